@@ -1,0 +1,68 @@
+"""Builds the native libraries of backburner_amd in-tree (hipcc cross-compiles gfx950; no GPU needed).
+
+    python -m backburner_amd.build          # libpa_hip.so, libpa_synth.so, oracle/liboracle.so (+ oracle/_ref)
+
+libpa_hip.so   the product: HIP kernels + the C ABI of include/phone_attn_hip.h
+libpa_synth.so bench/test support: synthetic HBM pages, device memory and event plumbing
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = ROOT / "_build"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+    # packed fp32 VALU forms stay off (hipcc forms them by itself otherwise); fp16 packed math is unaffected
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # IEEE fp32 division: the device q8_0 quantizer must round exactly like the reference's (d = amax/127, id = 1/d)
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+]
+
+LIBS = {
+    "libpa_hip.so": ["pa_attn.hip", "pa_accept.hip", "pa_abi.cpp"],
+    "libpa_synth.so": ["pa_synth.hip"],
+}
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(x for x in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in x)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def build(verbose: bool = False) -> None:
+    BUILD.mkdir(exist_ok=True)
+    jobs = []
+    for lib, srcs in LIBS.items():
+        for s in srcs:
+            obj = BUILD / (s + ".o")
+            lang = ["-x", "hip"] if s.endswith(".hip") else []
+            jobs.append([HIPCC, *HIP_FLAGS, *lang, "-c", str(CSRC / s), "-o", str(obj)])
+    with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), jobs))
+    for lib, srcs in LIBS.items():
+        objs = [str(BUILD / (s + ".o")) for s in srcs]
+        tmp = PKG / (lib + ".tmp")
+        _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
+        os.replace(tmp, PKG / lib)
+    # the oracle (test infrastructure) and, where the reference checkout exists, its pa-tool builds
+    _run(["make", "-s", "-C", str(ROOT / "oracle")], verbose)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print("built:", ", ".join(sorted(p.name for p in PKG.glob("*.so"))))

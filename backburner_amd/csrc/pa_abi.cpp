@@ -1,0 +1,393 @@
+// pa_abi.cpp - the C ABI of libpa_hip.so (declared in include/phone_attn_hip.h): the reference's sme_* entry points
+// (phone-attn.h:63-71) and the device-resident engine path. Host C++ over the HIP runtime; all compute runs in the HIP
+// kernels of pa_attn.hip / pa_accept.hip. There is no CPU fallback: without a gfx950 device every call fails loudly.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/phone_attn_hip.h"
+#include "pa_attn.h"
+
+using namespace pa_hip;
+
+namespace {
+
+thread_local std::string g_err;
+
+void set_err(const std::string & e) { g_err = e; }
+bool hip_ok(hipError_t e, const char * what) {
+    if (e == hipSuccess) return true;
+    set_err(std::string(what) + ": " + hipGetErrorString(e));
+    return false;
+}
+
+// ---------------------------------------------------------------- device check (once per process)
+int g_dev_state = -1;   // -1 unknown, 0 unusable, 1 usable
+std::string g_dev_why;
+std::mutex g_dev_mu;
+
+bool device_usable() {
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if (g_dev_state >= 0) return g_dev_state == 1;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void) hipGetLastError();
+        g_dev_state = 0; g_dev_why = "no HIP device";
+        return false;
+    }
+    int dev = 0;
+    (void) hipGetDevice(&dev);
+    hipDeviceProp_t pr;
+    if (hipGetDeviceProperties(&pr, dev) != hipSuccess || std::strncmp(pr.gcnArchName, "gfx950", 6) != 0) {
+        g_dev_state = 0; g_dev_why = std::string("device is not gfx950: ") + pr.gcnArchName;
+        return false;
+    }
+    g_dev_state = 1;
+    return true;
+}
+
+uint32_t head_bytes(int fmt, int hd) {
+    return fmt == PA_FMT_Q8_0 ? (uint32_t) (hd / 32 * 34) : fmt == PA_FMT_Q4_0 ? (uint32_t) (hd / 32 * 18) : (uint32_t) (hd * 2);
+}
+
+template <typename T> bool ensure(T *& p, size_t & cap, size_t need_bytes, const char * what) {
+    if (need_bytes <= cap && p) return true;
+    if (p) { (void) hipDeviceSynchronize(); (void) hipFree(p); p = nullptr; cap = 0; }
+    const size_t sz = std::max<size_t>(need_bytes, 256);
+    if (!hip_ok(hipMalloc((void **) &p, sz), what)) return false;
+    cap = sz;
+    return true;
+}
+
+int env_int(const char * name, int def) { const char * e = getenv(name); return e ? atoi(e) : def; }
+
+}  // namespace
+
+// ---------------------------------------------------------------- the workspace
+struct pa_hip_ws {
+    int device = 0;
+    _Float16 * q16 = nullptr; size_t q16_cap = 0;
+    float * po = nullptr; size_t po_cap = 0;
+    float2 * pml = nullptr; size_t pml_cap = 0;
+    unsigned long long * apart = nullptr; size_t apart_cap = 0;
+    unsigned int * acount = nullptr;
+    // the sme_* compatibility path: its own stream and staging buffers
+    hipStream_t stream = nullptr;
+    uint8_t * dk = nullptr; size_t dk_cap = 0;
+    uint8_t * dv = nullptr; size_t dv_cap = 0;
+    float * dq = nullptr; size_t dq_cap = 0;
+    float * dout = nullptr; size_t dout_cap = 0;
+    // measurement hook (pa_hip_ws_time_next)
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
+    if (!device_usable()) { set_err("pa_hip_ws_new: " + g_dev_why); return nullptr; }
+    if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return nullptr;
+    pa_hip_ws * w = new pa_hip_ws();
+    w->device = device;
+    if (!hip_ok(hipMalloc((void **) &w->acount, 256), "hipMalloc counter") ||
+        !hip_ok(hipMemset(w->acount, 0, 256), "hipMemset counter")) {   // once, at creation; the kernel keeps it zero
+        delete w;
+        return nullptr;
+    }
+    return w;
+}
+
+extern "C" void pa_hip_ws_destroy(pa_hip_ws * w) {
+    if (!w) return;
+    (void) hipDeviceSynchronize();
+    hipFree(w->q16); hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
+    hipFree(w->dk); hipFree(w->dv); hipFree(w->dq); hipFree(w->dout);
+    if (w->stream) hipStreamDestroy(w->stream);
+    delete w;
+}
+
+extern "C" const char * pa_hip_last_error(void) { return g_err.c_str(); }
+
+extern "C" int pa_hip_ws_time_next(pa_hip_ws * ws, void * ev_start, void * ev_end) {
+    if (!ws) { set_err("pa_hip_ws_time_next: null workspace"); return -1; }
+    ws->ev0 = (hipEvent_t) ev_start; ws->ev1 = (hipEvent_t) ev_end;
+    return 0;
+}
+
+extern "C" int pa_hip_alloc_page(size_t bytes, void ** k, void ** v) {
+    if (!k || !v) { set_err("pa_hip_alloc_page: null output"); return -1; }
+    *k = *v = nullptr;
+    if (!device_usable()) { set_err("pa_hip_alloc_page: " + g_dev_why); return -1; }
+    if (!hip_ok(hipMalloc(k, bytes), "hipMalloc page K")) return -1;
+    if (!hip_ok(hipMalloc(v, bytes), "hipMalloc page V")) { hipFree(*k); *k = nullptr; return -1; }
+    return 0;
+}
+
+extern "C" void pa_hip_free_page(void * k, void * v) {
+    if (k) hipFree(k);
+    if (v) hipFree(v);
+}
+
+// ---------------------------------------------------------------- the engine path
+namespace {
+
+int pick_cfg(uint32_t rows, uint32_t hd) {
+    const int forced = env_int("PA_HIP_CFG", -1);
+    if (forced >= 0 && forced <= CFG_PREFILL) return forced;
+    if (rows <= 16) return CFG_DECODE;
+    if (rows <= 64) return CFG_MID;
+    if (rows <= 128 || hd == 256) return CFG_VERIFY;
+    return CFG_PREFILL;
+}
+
+}  // namespace
+
+extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+                           const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, void * stream) {
+    if (!ws || !s) { set_err("pa_hip_attn: null workspace or shape"); return -1; }
+    if (s->hd != 128 && s->hd != 256) { set_err("pa_hip_attn: hd must be 128 or 256"); return -1; }
+    if (s->fmt > PA_FMT_Q4_0) { set_err("pa_hip_attn: fmt must be 0 (f16), 1 (q8_0) or 2 (q4_0)"); return -1; }
+    if (s->qmode > PA_QMODE_F16) { set_err("pa_hip_attn: qmode must be 0 (ggml) or 1 (f16)"); return -1; }
+    if (s->nkv == 0 || s->rows == 0) { set_err("pa_hip_attn: nkv and rows must be > 0"); return -1; }
+    const uint32_t hbmin = head_bytes((int) s->fmt, (int) s->hd);
+    if (s->hb < hbmin || (uint64_t) s->rs < (uint64_t) s->nkv * s->hb) {
+        set_err("pa_hip_attn: hb " + std::to_string(s->hb) + " / rs " + std::to_string(s->rs) + " too small for nkv " +
+                std::to_string(s->nkv) + " heads of " + std::to_string(hbmin) + " bytes");
+        return -1;
+    }
+    if (n_pages < 0 || (n_pages > 0 && (!k_pages || !v_pages || !nkeys))) { set_err("pa_hip_attn: bad page table"); return -1; }
+    if (!Q || !O || !m || !l) { set_err("pa_hip_attn: null Q/O/m/l"); return -1; }
+    if (((uintptr_t) O & 15) || ((uintptr_t) Q & 3)) { set_err("pa_hip_attn: O must be 16-byte and Q 4-byte aligned"); return -1; }
+    uint64_t total = 0;
+    for (int i = 0; i < n_pages; i++) {
+        if (nkeys[i] > 0 && (!k_pages[i] || !v_pages[i])) { set_err("pa_hip_attn: null page " + std::to_string(i)); return -1; }
+        total += nkeys[i];
+    }
+    if (total > 0xffffffffull) { set_err("pa_hip_attn: more than 2^32 keys"); return -1; }
+    hipStream_t st = (hipStream_t) stream;
+
+    const int cfg = pick_cfg(s->rows, s->hd);
+    int rows_wg = 16, nb = 64;
+    cfg_geometry(cfg, (int) s->hd, rows_wg, nb);
+    const uint32_t nrb = (s->rows + rows_wg - 1) / rows_wg, qr = nrb * rows_wg;
+    const uint32_t units = s->nkv * nrb;
+
+    // split-K chunking per launch (pages go in groups of MAXP): aim at ~4 workgroups per CU for the memory-bound shapes
+    // and one per CU for the row-heavy ones; a chunk is a multiple of the key tile
+    const int target = env_int("PA_HIP_TARGET_WG", cfg == CFG_DECODE || cfg == CFG_MID ? 1024 : cfg == CFG_VERIFY ? 768 : 256);
+    const int forced_chunk = env_int("PA_HIP_CHUNK", 0);
+    struct launch_t { int p0, np; uint32_t keys, chunk, n_chunks, slot0; };
+    std::vector<launch_t> L;
+    uint32_t n_slots = 0;
+    for (int p0 = 0; p0 < n_pages; p0 += MAXP) {
+        const int np = std::min(MAXP, n_pages - p0);
+        uint32_t keys = 0;
+        for (int i = 0; i < np; i++) keys += nkeys[p0 + i];
+        if (keys == 0) continue;
+        uint32_t chunk;
+        if (forced_chunk > 0) chunk = (uint32_t) forced_chunk;
+        else {
+            const uint32_t want = std::max<uint32_t>(1, (uint32_t) target / units);
+            chunk = (keys + want - 1) / want;
+        }
+        chunk = std::max<uint32_t>((uint32_t) nb, (chunk + nb - 1) / nb * nb);
+        const uint32_t nch = (keys + chunk - 1) / chunk;
+        L.push_back({p0, np, keys, chunk, nch, n_slots});
+        n_slots += nch;
+    }
+
+    // buffers
+    const size_t q16_b = (size_t) s->nkv * qr * s->hd * sizeof(_Float16);
+    const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
+    const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
+    if (!ensure(ws->q16, ws->q16_cap, q16_b, "hipMalloc q16") || !ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") ||
+        !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
+        return -1;
+
+    // Q -> fp16 rows (q8_0-rounded in ggml mode)
+    QprepArgs qa;
+    qa.q = Q; qa.q16 = ws->q16; qa.nkv = s->nkv; qa.rows = s->rows; qa.qr = qr; qa.hd = s->hd; qa.qmode = s->qmode; qa.scale = s->scale;
+    if (!hip_ok(launch_qprep(qa, st), "qprep launch")) return -1;
+
+    const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
+    ws->ev0 = ws->ev1 = nullptr;
+    if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
+    for (const launch_t & ln : L) {
+        AttnArgs a;
+        std::memset(&a, 0, sizeof a);
+        uint32_t acc = 0;
+        for (int i = 0; i < ln.np; i++) {
+            a.kp[i] = (const uint8_t *) k_pages[ln.p0 + i];
+            a.vp[i] = (const uint8_t *) v_pages[ln.p0 + i];
+            a.pstart[i] = acc;
+            acc += nkeys[ln.p0 + i];
+        }
+        a.pstart[ln.np] = acc;
+        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.chunk;
+        a.n_items = ln.n_chunks * units;
+        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
+        a.s_mul = (s->qmode == PA_QMODE_GGML ? s->scale : 1.0f) * 1.4426950408889634f;
+        a.q16 = ws->q16; a.po = ws->po; a.pml = ws->pml;
+        const uint32_t grid = (a.n_items + 7) / 8 * 8;
+        if (!hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch")) return -1;
+    }
+    if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
+
+    MergeArgs ma;
+    ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
+    ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+    if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
+    return 0;
+}
+
+extern "C" int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, int64_t vocab, const int32_t * draft, int32_t * out,
+                             void * stream) {
+    if (!ws || !logits || !out || (n_rows > 1 && !draft)) { set_err("pa_hip_accept: null argument"); return -1; }
+    if (n_rows < 1 || n_rows > 64) { set_err("pa_hip_accept: n_rows must be 1..64"); return -1; }
+    if (vocab < 1 || vocab > 0x7fffffffLL) { set_err("pa_hip_accept: vocab must be 1..2^31-1"); return -1; }
+    if ((vocab & 3) == 0 && ((uintptr_t) logits & 15)) { set_err("pa_hip_accept: logits must be 16-byte aligned"); return -1; }
+    // about 256 workgroups in total, each slice at least 4096 values
+    int splits = std::max(1, std::min(256 / n_rows, (int) ((vocab + 4095) / 4096)));
+    splits = std::min(splits, env_int("PA_HIP_ACCEPT_SPLITS", splits));
+    const size_t need = (size_t) n_rows * splits * sizeof(unsigned long long);
+    if (!ensure(ws->apart, ws->apart_cap, need, "hipMalloc accept partials")) return -1;
+    AcceptArgs a;
+    a.logits = logits; a.draft = draft; a.out = out; a.part = ws->apart; a.counter = ws->acount;
+    a.vocab = vocab; a.n_rows = n_rows; a.splits = splits;
+    return hip_ok(launch_accept(a, (hipStream_t) stream), "accept launch") ? 0 : -1;
+}
+
+extern "C" int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream) {
+    if (fmt != PA_FMT_Q8_0 && fmt != PA_FMT_Q4_0) { set_err("pa_hip_quantize: fmt must be 1 or 2"); return -1; }
+    if (n < 0 || n % 32 || (n > 0 && (!x || !y))) { set_err("pa_hip_quantize: n must be a multiple of 32"); return -1; }
+    return hip_ok(launch_quantize(fmt, x, y, n, (hipStream_t) stream), "quantize launch") ? 0 : -1;
+}
+
+// ---------------------------------------------------------------- 1. the reference C ABI
+namespace {
+
+std::atomic<int> g_nr{0}, g_hd{0};
+void compat_shape(int & nr, int & hd) {
+    if (g_nr.load() == 0) {
+        const int a = env_int("PA_NR", 48), b = env_int("PA_HD", 256);
+        int z = 0;
+        g_nr.compare_exchange_strong(z, a);
+        z = 0;
+        g_hd.compare_exchange_strong(z, b);
+    }
+    nr = g_nr.load(); hd = g_hd.load();
+}
+
+bool is_device_ptr(const void * p) {
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) { (void) hipGetLastError(); return false; }
+    return at.type == hipMemoryTypeDevice;
+}
+
+void fail_out(float * O, float * m, float * l, size_t rows, int hd) {
+    if (O) std::memset(O, 0, sizeof(float) * rows * (size_t) hd);
+    for (size_t r = 0; r < rows; r++) { if (m) m[r] = -INFINITY; if (l) l[r] = 0.0f; }
+}
+
+// one synchronous call of the engine path for `nkv` heads at K/V (host or device), reference rounding (f16 Q*scale)
+bool compat_call(pa_hip_ws * w, const float * Q, int qrs, int qhs, const uint8_t * K, const uint8_t * V, size_t rs, size_t hb,
+                 int fmt, int nkv, int nk, float scale, float * O, float * m, float * l) {
+    int NR, HD;
+    compat_shape(NR, HD);
+    const size_t rows = (size_t) nkv * NR;
+    if (!w) { set_err("sme_*: null workspace"); return false; }
+    if (fmt < 0 || fmt > 2) { set_err("sme_*: is_q8 must be 0, 1 or 2"); return false; }
+    if (nk < 0) { set_err("sme_*: nk < 0"); return false; }
+    if (nk == 0) {   // sme_attn.c:281-282: m starts at -1e30, l and O at 0
+        std::memset(O, 0, sizeof(float) * rows * HD);
+        for (size_t r = 0; r < rows; r++) { m[r] = -1e30f; l[r] = 0.0f; }
+        return true;
+    }
+    if (!w->stream && !hip_ok(hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking), "hipStreamCreate")) return false;
+    hipStream_t st = w->stream;
+    const uint32_t hbmin = head_bytes(fmt, HD);
+    // K/V: device pointers are used in place; host rows are staged (rows [0, nk) of every head in the span)
+    const size_t span = (size_t) (nk - 1) * rs + (size_t) (nkv - 1) * hb + hbmin;
+    const uint8_t * dK = K, * dV = V;
+    if (!is_device_ptr(K)) {
+        if (!ensure(w->dk, w->dk_cap, span, "hipMalloc K staging") ||
+            !hip_ok(hipMemcpyAsync(w->dk, K, span, hipMemcpyHostToDevice, st), "K upload"))
+            return false;
+        dK = w->dk;
+    }
+    if (!is_device_ptr(V)) {
+        if (!ensure(w->dv, w->dv_cap, span, "hipMalloc V staging") ||
+            !hip_ok(hipMemcpyAsync(w->dv, V, span, hipMemcpyHostToDevice, st), "V upload"))
+            return false;
+        dV = w->dv;
+    }
+    const size_t q_b = rows * HD * sizeof(float), o_b = rows * (HD + 2) * sizeof(float);
+    if (!ensure(w->dq, w->dq_cap, q_b, "hipMalloc Q staging") || !ensure(w->dout, w->dout_cap, o_b, "hipMalloc O staging")) return false;
+    for (int h = 0; h < nkv; h++)
+        if (!hip_ok(hipMemcpy2DAsync(w->dq + (size_t) h * NR * HD, HD * sizeof(float), Q + (size_t) h * qhs, (size_t) qrs * sizeof(float),
+                                     HD * sizeof(float), NR, hipMemcpyHostToDevice, st), "Q upload"))
+            return false;
+    pa_hip_shape s;
+    s.nkv = (uint32_t) nkv; s.rows = (uint32_t) NR; s.hd = (uint32_t) HD; s.fmt = (uint32_t) fmt;
+    s.rs = (uint32_t) rs; s.hb = (uint32_t) hb; s.qmode = PA_QMODE_F16; s.scale = scale;
+    if (nkv == 1) { s.hb = hbmin; if (s.rs < s.hb) s.rs = s.hb; }
+    const void * kp[1] = {dK}, * vp[1] = {dV};
+    const uint32_t nkeys[1] = {(uint32_t) nk};
+    float * dO = w->dout, * dm = dO + rows * HD, * dl = dm + rows;
+    if (pa_hip_attn(w, &s, kp, vp, nkeys, 1, w->dq, dO, dm, dl, st) != 0) return false;
+    if (!hip_ok(hipMemcpyAsync(O, dO, rows * HD * sizeof(float), hipMemcpyDeviceToHost, st), "O download") ||
+        !hip_ok(hipMemcpyAsync(m, dm, rows * sizeof(float), hipMemcpyDeviceToHost, st), "m download") ||
+        !hip_ok(hipMemcpyAsync(l, dl, rows * sizeof(float), hipMemcpyDeviceToHost, st), "l download") ||
+        !hip_ok(hipStreamSynchronize(st), "sme_* call"))
+        return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" int pa_hip_set_compat_shape(int nr, int hd) {
+    if (nr < 1 || nr > 4096 || (hd != 128 && hd != 256)) { set_err("pa_hip_set_compat_shape: nr 1..4096, hd 128 or 256"); return -1; }
+    g_nr.store(nr); g_hd.store(hd);
+    return 0;
+}
+
+extern "C" void * sme_ws_new(void) {
+    int dev = 0;
+    if (!device_usable()) { set_err("sme_ws_new: " + g_dev_why); return nullptr; }
+    (void) hipGetDevice(&dev);
+    return pa_hip_ws_new(dev);
+}
+
+extern "C" void * sme_pipe_new(int nh) { (void) nh; return sme_ws_new(); }
+
+extern "C" void pa_hip_ws_free(void * w) { pa_hip_ws_destroy((pa_hip_ws *) w); }
+
+extern "C" int sme2_available(void) { return device_usable() ? 1 : 0; }
+
+extern "C" void sme_attn_partial(void * w, const float * Q, int qrs, const uint8_t * K, const uint8_t * V, size_t rs,
+                                 int is_q8, int nk, float scale, int bk, float * O, float * m, float * l) {
+    (void) bk;
+    int NR, HD;
+    compat_shape(NR, HD);
+    if (!compat_call((pa_hip_ws *) w, Q, qrs, 0, K, V, rs, 0, is_q8, 1, nk, scale, O, m, l)) {
+        fprintf(stderr, "sme_attn_partial (libpa_hip): %s\n", g_err.c_str());
+        fail_out(O, m, l, (size_t) NR, HD);
+    }
+}
+
+extern "C" void sme_attn_pipe(void ** pp, int nw, int nh, const float * Q, const uint8_t * K, const uint8_t * V, size_t rs,
+                              size_t hb, int is_q8, int nkv, int nk, float scale, float * O, float * m, float * l) {
+    (void) nw; (void) nh;
+    int NR, HD;
+    compat_shape(NR, HD);
+    pa_hip_ws * w = pp ? (pa_hip_ws *) pp[0] : nullptr;
+    if (!compat_call(w, Q, HD, NR * HD, K, V, rs, hb, is_q8, nkv, nk, scale, O, m, l)) {
+        fprintf(stderr, "sme_attn_pipe (libpa_hip): %s\n", g_err.c_str());
+        fail_out(O, m, l, (size_t) nkv * NR, HD);
+    }
+}

@@ -1,0 +1,157 @@
+// pa_synth.hip - libpa_synth.so: device-side synthetic workloads and plumbing for bench.py and the GPU tests.
+// Not part of the path: it fills HBM pages with seeded q8_0/q4_0/f16 rows (so 64 layers of 285 MB need no host
+// generation or PCIe upload), and wraps the few HIP runtime calls the Python side needs (device memory, copies,
+// events), so bench.py and the tests run without torch.
+//
+// The value stream is the oracle's (oracle/pa_oracle.c orc_normal / orc_fill_rows): element i of stream `seed` is
+// Box-Muller over splitmix64 word i/2 (cos for even i, sin for odd), in double precision; blocks are quantized with the
+// ggml reference semantics (quantize_row_q8_0_ref / quantize_row_q4_0_ref).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstring>
+
+namespace {
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t stream_word(uint64_t seed, uint64_t p) {
+    return mix64(mix64(seed + 0x9e3779b97f4a7c15ull) + (p + 1) * 0x9e3779b97f4a7c15ull);
+}
+__device__ __forceinline__ float normal_at(uint64_t seed, int64_t i) {
+    const uint64_t w = stream_word(seed, (uint64_t) (i >> 1));
+    const double u1 = (double) ((w >> 40) + 1) * (1.0 / 16777216.0);
+    const double u2 = (double) ((w >> 16) & 0xffffffu) * (1.0 / 16777216.0);
+    const double r = sqrt(-2.0 * log(u1)), t = 6.283185307179586476925 * u2;
+    return (float) ((i & 1) ? r * sin(t) : r * cos(t));
+}
+
+__global__ void normal_kernel(float * out, int64_t n, uint64_t seed, int64_t i0, float amp) {
+    const int64_t k = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (k < n) out[k] = normal_at(seed, i0 + k) * amp;
+}
+
+// one thread per (key, head, 32-block)
+__global__ void fill_rows_kernel(uint8_t * rows, int fmt, int nkv, int hd, uint32_t rs, uint32_t hb, int64_t j0, int64_t n_keys,
+                                 uint64_t seed, float amp, int n_out, const int32_t * ch, float mul) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int nblk = hd / 32;
+    if (t >= n_keys * nkv * nblk) return;
+    const int blk = (int) (t % nblk), h = (int) ((t / nblk) % nkv);
+    const int64_t jj = t / nblk / nkv, j = j0 + jj;
+    float x[32];
+    const int64_t base = (j * nkv + h) * hd + blk * 32;
+    for (int e = 0; e < 32; e++) {
+        float v = normal_at(seed, base + e) * amp;
+        for (int o = 0; o < n_out; o++) if (ch[h * n_out + o] == blk * 32 + e) v *= mul;
+        x[e] = v;
+    }
+    uint8_t * dst = rows + (size_t) jj * rs + (size_t) h * hb;
+    if (fmt == 1) {
+        uint8_t * o = dst + blk * 34;
+        float amax = 0.0f;
+        for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(x[e]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = __builtin_bit_cast(uint16_t, (_Float16) d);
+        o[0] = (uint8_t) (dh & 0xff); o[1] = (uint8_t) (dh >> 8);
+        for (int e = 0; e < 32; e++) o[2 + e] = (uint8_t) (int8_t) roundf(x[e] * id);
+    } else if (fmt == 2) {
+        uint8_t * o = dst + blk * 18;
+        float amax = 0.0f, mx = 0.0f;
+        for (int e = 0; e < 32; e++) if (amax < fabsf(x[e])) { amax = fabsf(x[e]); mx = x[e]; }
+        const float d = mx / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = __builtin_bit_cast(uint16_t, (_Float16) d);
+        o[0] = (uint8_t) (dh & 0xff); o[1] = (uint8_t) (dh >> 8);
+        for (int e = 0; e < 16; e++) {
+            int q0 = (int8_t) (x[e] * id + 8.5f), q1 = (int8_t) (x[16 + e] * id + 8.5f);
+            q0 = q0 > 15 ? 15 : q0;
+            q1 = q1 > 15 ? 15 : q1;
+            o[2 + e] = (uint8_t) (q0 | (q1 << 4));
+        }
+    } else {
+        uint16_t * o = (uint16_t *) (dst + blk * 64);
+        for (int e = 0; e < 32; e++) o[e] = __builtin_bit_cast(uint16_t, (_Float16) x[e]);
+    }
+}
+
+// streaming copy: the bandwidth reference for the roofline, and the known-size kernel the FETCH_SIZE/WRITE_SIZE counters
+// are scaled by
+__global__ __launch_bounds__(256) void copy_kernel(const uint4 * __restrict__ src, uint4 * __restrict__ dst, int64_t n16) {
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t) gridDim.x * 256) dst[i] = src[i];
+}
+// read-only stream (sum of words, written once per block so nothing is optimised away)
+__global__ __launch_bounds__(256) void read_kernel(const uint4 * __restrict__ src, int64_t n16, uint32_t * __restrict__ sink) {
+    uint32_t acc = 0;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t) gridDim.x * 256) {
+        const uint4 v = src[i];
+        acc ^= v.x + v.y + v.z + v.w;
+    }
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;   // practically never taken, keeps the loads live
+}
+
+}  // namespace
+
+extern "C" {
+
+int pa_synth_normal(float * out, int64_t n, uint64_t seed, int64_t i0, float amp, void * stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(normal_kernel, dim3((uint32_t) ((n + 255) / 256)), dim3(256), 0, (hipStream_t) stream, out, n, seed, i0, amp);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int pa_synth_fill_rows(void * rows, int fmt, int nkv, int hd, uint32_t rs, int64_t j0, int64_t n_keys, uint64_t seed, float amp,
+                       int n_out, const int32_t * ch_dev, float mul, void * stream) {
+    const uint32_t hb = fmt == 1 ? (uint32_t) (hd / 32 * 34) : fmt == 2 ? (uint32_t) (hd / 32 * 18) : (uint32_t) (hd * 2);
+    const int64_t n = n_keys * nkv * (hd / 32);
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(fill_rows_kernel, dim3((uint32_t) ((n + 255) / 256)), dim3(256), 0, (hipStream_t) stream, (uint8_t *) rows,
+                       fmt, nkv, hd, rs, hb, j0, n_keys, seed, amp, n_out, ch_dev, mul);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int pa_synth_copy(const void * src, void * dst, int64_t bytes, int blocks, void * stream) {
+    hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(256), 0, (hipStream_t) stream, (const uint4 *) src, (uint4 *) dst, bytes / 16);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int pa_synth_read(const void * src, int64_t bytes, int blocks, uint32_t * sink, void * stream) {
+    hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t) stream, (const uint4 *) src, bytes / 16, sink);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// ---- plumbing
+void * pa_synth_malloc(size_t bytes) { void * p = nullptr; return hipMalloc(&p, bytes) == hipSuccess ? p : nullptr; }
+int pa_synth_free(void * p) { return hipFree(p) == hipSuccess ? 0 : -1; }
+int pa_synth_memset(void * p, int v, size_t bytes) { return hipMemset(p, v, bytes) == hipSuccess ? 0 : -1; }
+int pa_synth_h2d(void * dst, const void * src, size_t bytes) { return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1; }
+int pa_synth_d2h(void * dst, const void * src, size_t bytes) { return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1; }
+int pa_synth_sync(void) { return hipDeviceSynchronize() == hipSuccess ? 0 : -1; }
+const char * pa_synth_error(void) { return hipGetErrorString(hipGetLastError()); }
+int pa_synth_device_name(char * out, int n) {
+    hipDeviceProp_t pr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&pr, dev) != hipSuccess) return -1;
+    std::strncpy(out, pr.gcnArchName, (size_t) n - 1);
+    out[n - 1] = 0;
+    return pr.multiProcessorCount;
+}
+void * pa_synth_stream_new(void) {
+    hipStream_t s = nullptr;
+    return hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess ? (void *) s : nullptr;
+}
+int pa_synth_stream_sync(void * s) { return hipStreamSynchronize((hipStream_t) s) == hipSuccess ? 0 : -1; }
+void * pa_synth_event_new(void) { hipEvent_t e = nullptr; return hipEventCreate(&e) == hipSuccess ? (void *) e : nullptr; }
+int pa_synth_event_record(void * e, void * s) { return hipEventRecord((hipEvent_t) e, (hipStream_t) s) == hipSuccess ? 0 : -1; }
+float pa_synth_event_ms(void * a, void * b) {
+    float ms = -1.0f;
+    if (hipEventSynchronize((hipEvent_t) b) != hipSuccess) return -1.0f;
+    return hipEventElapsedTime(&ms, (hipEvent_t) a, (hipEvent_t) b) == hipSuccess ? ms : -1.0f;
+}
+int pa_synth_event_free(void * e) { return hipEventDestroy((hipEvent_t) e) == hipSuccess ? 0 : -1; }
+
+}  // extern "C"

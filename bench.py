@@ -1,0 +1,299 @@
+"""bench.py - phone-attn old-KV partial attention on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary] [--no-cpu]
+
+Headline workload: decode at long context, 64 layers in sequence, each layer = 1 query token x 64
+query heads over 8 KV heads (GQA 8), head dim 128, 131,072 old q8_0 positions in 32 pages of 4,096 keys, K with 4 x8
+outlier channels per head, 64 distinct seeded caches (18.25 GB in HBM, made on the device by libpa_synth). A step is
+one pass over the 64 layers: per layer one pa_hip_attn call (Q prep + split-K attention + merge) on one stream.
+
+Printed: ONE JSON line. value = microseconds per layer (lower is better); roofline = the attention kernel's
+algorithmic bytes per launch / its mean duration (HIP events recorded by the library around that kernel, on its
+stream); cpu_baseline = the oracle's ggml-faithful restatement (oracle/pa_oracle.c, OpenMP over rows) timed on this
+host's cores over a bounded sample of layer 0's keys and scaled to a full layer. --secondary adds the other BASELINE
+configs (4k decode, 16-token verify, 512-token prefill, q4_0 decode/verify, fused acceptance) as "secondary" entries.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E nameplate
+FP16_PEAK_TFS = 2516.6         # MI355X dense fp16 MFMA nameplate
+PAGE = 4096
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- workload
+class Layers:
+    """n_layers distinct seeded caches: per layer one K slab and one V slab of n_keys rows, viewed as PAGE-key pages."""
+
+    def __init__(self, bb, fmt, n_layers, n_keys, nkv=8, hd=128, rows=8, seed=0x5eed, outliers=4):
+        self.bb, self.fmt, self.n_layers, self.n_keys, self.nkv, self.hd, self.rows = bb, fmt, n_layers, n_keys, nkv, hd, rows
+        self.hb = bb.head_bytes(fmt, hd)
+        self.rs = nkv * self.hb
+        syn = bb.synth()
+        self.bufs = []
+        self.pages = []
+        self.q = []
+        import oracle as orc   # only for the outlier channel picks (a few ints), shared with the oracle generator
+        for L in range(n_layers):
+            kb, vb = bb.DeviceBuffer(n_keys * self.rs), bb.DeviceBuffer(n_keys * self.rs)
+            sk, sv, sq = seed + 1000 * L + 1, seed + 1000 * L + 2, seed + 1000 * L + 3
+            ch = bb.DeviceBuffer.from_array(orc.outlier_channels(sk, nkv, hd, outliers)) if outliers else None
+            if syn.pa_synth_fill_rows(kb.ptr, fmt, nkv, hd, self.rs, 0, n_keys, sk, 1.0, outliers, ch.ptr if ch else None, 8.0, None) \
+                    or syn.pa_synth_fill_rows(vb.ptr, fmt, nkv, hd, self.rs, 0, n_keys, sv, 1.0, 0, None, 1.0, None):
+                raise RuntimeError("synthetic fill failed")
+            qb = bb.DeviceBuffer(nkv * rows * hd * 4)
+            syn.pa_synth_normal(qb.ptr, nkv * rows * hd, sq, 0, 1.0, None)
+            np_ = (n_keys + PAGE - 1) // PAGE
+            self.pages.append(bb.Pages([kb.ptr + i * PAGE * self.rs for i in range(np_)],
+                                       [vb.ptr + i * PAGE * self.rs for i in range(np_)],
+                                       [min(PAGE, n_keys - i * PAGE) for i in range(np_)], []))
+            self.bufs += [kb, vb, qb] + ([ch] if ch else [])
+            self.q.append(qb)
+        bb.device_sync()
+        r = nkv * rows
+        self.out = bb.DeviceBuffer(r * hd * 4 + 2 * r * 4)
+        self.O, self.m, self.l = self.out.ptr, self.out.ptr + r * hd * 4, self.out.ptr + r * hd * 4 + r * 4
+        self.shape = bb.make_shape(nkv, rows, hd, fmt)
+
+    def kv_bytes(self):
+        return 2 * self.n_keys * self.rs
+
+    def alg_bytes(self):
+        """K/V + Q (fp32) + O, m, l (fp32): per layer."""
+        r = self.nkv * self.rows
+        return self.kv_bytes() + r * self.hd * 4 + r * self.hd * 4 + 2 * r * 4
+
+    def flops(self):
+        return 4.0 * self.nkv * self.rows * self.n_keys * self.hd
+
+    def close(self):
+        for b in self.bufs:
+            b.close()
+        self.out.close()
+
+
+def time_layers(bb, ws, lay: Layers, steps: int, warmup: int):
+    """W untimed steps, then K timed steps (each = every layer once); also the attention kernel alone per call."""
+    syn = bb.synth()
+    stream = syn.pa_synth_stream_new()
+    for _ in range(warmup):
+        for L in range(lay.n_layers):
+            ws.attn(lay.shape, lay.pages[L], lay.q[L].ptr, lay.O, lay.m, lay.l, stream)
+    syn.pa_synth_stream_sync(stream)
+    ev = [(syn.pa_synth_event_new(), syn.pa_synth_event_new()) for _ in range(steps * lay.n_layers)]
+    e0, e1 = syn.pa_synth_event_new(), syn.pa_synth_event_new()
+    bb.device_sync()
+    syn.pa_synth_event_record(e0, stream)
+    i = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for L in range(lay.n_layers):
+            ws.time_next(ev[i][0], ev[i][1])
+            ws.attn(lay.shape, lay.pages[L], lay.q[L].ptr, lay.O, lay.m, lay.l, stream)
+            i += 1
+    syn.pa_synth_event_record(e1, stream)
+    syn.pa_synth_stream_sync(stream)
+    bb.device_sync()
+    wall = time.perf_counter() - t0
+    total_ms = syn.pa_synth_event_ms(e0, e1)
+    kern = np.array([syn.pa_synth_event_ms(a, b) for a, b in ev])
+    for a, b in ev:
+        syn.pa_synth_event_free(a); syn.pa_synth_event_free(b)
+    syn.pa_synth_event_free(e0); syn.pa_synth_event_free(e1)
+    return total_ms, kern, wall
+
+
+def measured_copy_bw(bb, nbytes=2 << 30):
+    """Plain device-to-device copy and read-only stream of nbytes: the achievable-bandwidth reference."""
+    syn = bb.synth()
+    a, b = bb.DeviceBuffer(nbytes), bb.DeviceBuffer(nbytes)
+    sink = bb.DeviceBuffer(1 << 16)
+    syn.pa_synth_memset(a.ptr, 1, nbytes)
+    e0, e1 = syn.pa_synth_event_new(), syn.pa_synth_event_new()
+    res = {}
+    for name, fn, traffic in (("copy", lambda: syn.pa_synth_copy(a.ptr, b.ptr, nbytes, 4096, None), 2 * nbytes),
+                              ("read", lambda: syn.pa_synth_read(a.ptr, nbytes, 4096, sink.ptr, None), nbytes)):
+        fn(); fn()
+        bb.device_sync()
+        syn.pa_synth_event_record(e0, None)
+        for _ in range(10):
+            fn()
+        syn.pa_synth_event_record(e1, None)
+        ms = syn.pa_synth_event_ms(e0, e1) / 10
+        res[name] = traffic / (ms * 1e-3) / 1e9
+    for x in (a, b, sink):
+        x.close()
+    return res
+
+
+def cpu_baseline(bb, lay: Layers, sample_keys: int):
+    """Time the oracle's ggml-faithful CPU restatement on layer 0's first sample_keys keys, all rows, all host cores;
+    also check the GPU on exactly that sample against it."""
+    import oracle as orc
+    rs = lay.rs
+    kb = lay.bufs[0].download(np.uint8, sample_keys * rs)
+    vb = lay.bufs[1].download(np.uint8, sample_keys * rs)
+    q = lay.q[0].download(np.float32).reshape(-1, lay.hd)
+    s = orc.make_shape(lay.nkv, lay.rows, lay.hd, lay.fmt)
+    threads = len(os.sched_getaffinity(0))
+    t0 = time.perf_counter()
+    O, m, l = orc.attn_ggml(s, q, kb, vb, sample_keys, threads)
+    dt = time.perf_counter() - t0
+    # the GPU on the same sample (pages of the first sample_keys keys)
+    np_ = (sample_keys + PAGE - 1) // PAGE
+    pages = bb.Pages(lay.pages[0].k[:np_], lay.pages[0].v[:np_], [min(PAGE, sample_keys - i * PAGE) for i in range(np_)], [])
+    ws = bb.Workspace()
+    ws.attn(lay.shape, pages, lay.q[0].ptr, lay.O, lay.m, lay.l)
+    bb.device_sync()
+    r = lay.nkv * lay.rows
+    ml = lay.out.download(np.float32, 2 * r, offset=r * lay.hd * 4)
+    Og = lay.out.download(np.float32, r * lay.hd).reshape(r, lay.hd)
+    eo, em, el = orc.rel_err(Og, ml[:r], ml[r:], O, m, l)
+    ws.close()
+    per_layer_us = dt * 1e6 * lay.n_keys / sample_keys
+    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"layer 0, keys [0, {sample_keys}) of {lay.n_keys}, all {r} rows, oracle/pa_oracle.c orc_attn_ggml "
+                      f"(ggml-faithful, q8_0 int block dots, OpenMP {threads} threads) {dt:.2f} s, scaled x{lay.n_keys / sample_keys:g}",
+            }, {"max_rel_O": eo, "max_rel_m": em, "max_rel_l": el, "keys": sample_keys, "tol": 2e-3}
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
+    p = ROOT / "profiles" / f"{name}_pmc.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label):
+    lay = Layers(bb, fmt, n_layers, n_keys, rows=rows)
+    total_ms, kern, wall = time_layers(bb, ws, lay, steps, warmup)
+    per_layer_us = total_ms * 1e3 / (steps * n_layers)
+    kmean = float(kern.mean())
+    res = {"workload": label, "us_per_layer": round(per_layer_us, 3), "attn_kernel_us": round(kmean * 1e3, 3),
+           "attn_kernel_us_p90": round(float(np.percentile(kern, 90)) * 1e3, 3),
+           "gbs_kernel": round(lay.alg_bytes() / (kmean * 1e-3) / 1e9, 1),
+           "gbs_call": round(lay.alg_bytes() / (per_layer_us * 1e-6) / 1e9, 1),
+           "tflops_kernel": round(lay.flops() / (kmean * 1e-3) / 1e12, 2)}
+    res["hbm_frac_kernel"] = round(res["gbs_kernel"] / HBM_PEAK_GBS, 4)
+    res["mfma_frac_kernel"] = round(res["tflops_kernel"] / FP16_PEAK_TFS, 4)
+    return lay, res, total_ms, kern
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=64)
+    ap.add_argument("--secondary", action="store_true", help="also run the other BASELINE configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-keys", type=int, default=16384)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU position sharding is a design note only (DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import backburner_amd as bb
+    name = (bytes(64))
+    import ctypes as C
+    nb = C.create_string_buffer(64)
+    n_cu = bb.synth().pa_synth_device_name(nb, 64)
+    log(f"device {nb.value.decode()} CUs {n_cu}")
+    ws = bb.Workspace()
+    bw = measured_copy_bw(bb)
+    log(f"copy {bw['copy']:.0f} GB/s, read {bw['read']:.0f} GB/s")
+
+    lay, head, total_ms, kern = run_config(bb, ws, bb.FMT_Q8_0, args.layers, 131072, 8, args.steps, args.warmup,
+                                           "decode 1 token x 64 q-heads / 8 kv-heads, hd 128, 131072 q8_0 keys, 64 layers")
+    log("headline", json.dumps(head))
+    cpu, parity = (None, None) if args.no_cpu else cpu_baseline(bb, lay, args.cpu_keys)
+    lay.close()
+
+    secondary = []
+    if args.secondary:
+        for fmt, nl, nk, rows, label in (
+                (bb.FMT_Q8_0, 1, 4096, 8, "decode 4096 q8_0 keys (1 layer)"),
+                (bb.FMT_Q8_0, 64, 98304, 128, "verify 16 tokens, 98304 q8_0 keys, 64 layers"),
+                (bb.FMT_Q8_0, 64, 65536, 4096, "prefill 512 tokens, 65536 q8_0 keys, 64 distinct caches"),
+                (bb.FMT_Q4_0, 64, 143360, 8, "decode 143360 q4_0 keys, 64 layers"),
+                (bb.FMT_Q4_0, 64, 143360, 128, "verify 16 tokens, 143360 q4_0 keys, 64 layers")):
+            st = max(2, min(args.steps, 10)) if rows > 8 else args.steps
+            l2, r2, _, _ = run_config(bb, ws, fmt, nl, nk, rows, st, 1, label)
+            l2.close()
+            log("secondary", json.dumps(r2))
+            secondary.append(r2)
+        secondary.append(bench_accept(bb, ws, args.steps))
+
+    alg = 2 * 131072 * 8 * 136 + 64 * 128 * 4 * 2 + 64 * 8
+    kmean_s = float(kern.mean()) * 1e-3
+    achieved = alg / kmean_s / 1e9
+    out = {
+        "metric": "old-KV attn us/layer + % HBM BW at 128k Q8_0 decode; prefill-chunk TFLOP/s",
+        "value": head["us_per_layer"], "unit": "us/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q8_0 K/V, fp16 MFMA, fp32 softmax/accumulate", "data": "synthetic (seeded N(0,1), made on device)",
+        "config": {"workload": "decode at long context: 1 token, 64 query heads / 8 KV heads (GQA 8), head dim 128, "
+                               "131072 old q8_0 positions (32 pages of 4096), K with 4 x8 outlier channels per head",
+                   "layers": args.layers, "global_batch": 1, "seq_len": 131072, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode128k"),
+                     "kernel": "attn_kernel<128, q8_0, decode>", "alg_bytes_per_launch": alg,
+                     "kernel_us_mean": round(kmean_s * 1e6, 3)},
+        "hbm_frac_call": round(alg / (head["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "measured_bw_gbs": {k: round(v, 1) for k, v in bw.items()},
+        "cpu_baseline": cpu, "parity_vs_cpu": parity,
+    }
+    if secondary:
+        out["secondary"] = secondary
+    print(json.dumps(out), flush=True)
+
+
+def bench_accept(bb, ws, steps):
+    """Fused greedy acceptance, logits fp32 [17][151936]: mean kernel time over `steps` calls."""
+    syn = bb.synth()
+    rng = np.random.default_rng(17)
+    logits = rng.standard_normal((17, 151936)).astype(np.float32)
+    draft = rng.integers(0, 151936, 16).astype(np.int32)
+    k = int(rng.integers(0, 17))
+    for i in range(k):
+        logits[i, draft[i]] = logits[i].max() + 1
+    dl, dd, do = bb.DeviceBuffer.from_array(logits), bb.DeviceBuffer.from_array(draft), bb.DeviceBuffer(19 * 4)
+    for _ in range(3):
+        ws.accept(dl.ptr, 17, 151936, dd.ptr, do.ptr)
+    e0, e1 = syn.pa_synth_event_new(), syn.pa_synth_event_new()
+    bb.device_sync()
+    syn.pa_synth_event_record(e0, None)
+    for _ in range(steps):
+        ws.accept(dl.ptr, 17, 151936, dd.ptr, do.ptr)
+    syn.pa_synth_event_record(e1, None)
+    us = syn.pa_synth_event_ms(e0, e1) * 1e3 / steps
+    out = do.download(np.int32)
+    import oracle as orc
+    ko, bo, _ = orc.accept(logits, draft)
+    return {"workload": "fused greedy acceptance, logits fp32 [17][151936]", "us_per_call": round(us, 3),
+            "gbs": round(logits.nbytes / (us * 1e-6) / 1e9, 1), "bit_exact": bool(out[0] == ko and out[1] == bo),
+            "planted_k": k, "k": int(out[0])}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,124 @@
+/* phone_attn_hip.h - C ABI of libpa_hip.so: partial attention over the old, quantized KV cache on MI355X (gfx950).
+ *
+ * Two groups of entry points:
+ *
+ *  1. The reference's C ABI, same symbols, argument order and meaning as phone-attn/phone-attn.h:63-71 (the CPU engine
+ *     in scripts/sme/sme_attn.c:255-463), so pa::server / pa-tool link against this library unchanged. Buffers are host
+ *     memory (or device memory from pa_hip_alloc_page); calls are synchronous. The reference fixes the rows per KV head
+ *     and the head dim at compile time (NR = 48, HD = 256: phone-attn.h:78-79); here they default to 48/256 and
+ *     pa_hip_set_compat_shape() (or PA_NR / PA_HD in the environment) changes them. These functions return void, as in
+ *     the reference; a failure leaves m = -inf, l = 0, O = 0 (the reference GPU engine's failure value,
+ *     pa-metal.mm:932-937) and sets pa_hip_last_error().
+ *
+ *  2. The device-resident engine path: one launch sequence per call over a page table of HBM pages (the role of
+ *     pa::engine::begin/end, phone-attn.h:170-174, and of the Metal engine's encode_big, pa-metal.mm:674-714). All
+ *     tensors are device pointers, work is enqueued on the caller's stream, nothing is copied to the host.
+ *
+ * Row format (config_req.rs/hb/is_q8, phone-attn.h:88): key j, KV head h starts at page + j*rs + h*hb; q8_0 = 34-byte
+ * blocks (fp16 d, 32 int8), q4_0 = 18-byte blocks (fp16 d, byte i = element i low nibble, element i+16 high nibble),
+ * f16 = hd halves. Q is fp32 [nkv][rows][hd], unscaled; O is fp32 [nkv][rows][hd] unnormalised, m and l fp32
+ * [nkv][rows] with O = sum_j e^(s_j-m) v_j, l = sum_j e^(s_j-m), m = max_j s_j, s_j = scale*q.k_j
+ * (sme_attn.c:3-5); no keys -> (0, -inf, 0).
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- 1. reference C ABI (phone-attn.h:63-71) */
+
+/* sme_attn.c:255 sme_ws_new: one workspace per calling thread (here: a HIP stream and staging buffers). Never freed by
+ * the reference's callers; pa_hip_ws_free() releases one. */
+void * sme_ws_new(void);
+
+/* sme_attn.c:271-306 sme_attn_partial: ONE KV head. Q fp32 [NR][HD] with row stride qrs floats (unscaled); K, V point at
+ * key 0's row of this head (base + h*hb); rs = row stride in bytes; is_q8 0 f16 / 1 q8_0 / 2 q4_0; nk keys (the
+ * reference requires a multiple of 64; any nk >= 0 works here); bk is accepted and ignored (the GPU kernel tiles
+ * itself). Writes O [NR][HD], m [NR], l [NR]. Rounding follows the reference engines: Q as f16(q*scale), K/V
+ * dequantized to fp16, fp32 accumulation. An empty call returns m = -1e30 (sme_attn.c:281). */
+void sme_attn_partial(void * w, const float * Q, int qrs, const uint8_t * K, const uint8_t * V, size_t rs,
+                      int is_q8, int nk, float scale, int bk, float * O, float * m, float * l);
+
+/* phone-attn.h:67: 1 if the engine can run (a gfx950 device is present and the library initialised on it). The
+ * server routes non-GPU pages to the sme_* calls only when this returns 1 (phone-attn.h:588, 593). */
+int sme2_available(void);
+
+/* sme_attn.c:419 sme_pipe_new(nh): a pipelined-engine handle; here the same object as sme_ws_new (nh is ignored). */
+void * sme_pipe_new(int nh);
+
+/* sme_attn.c:437-463 sme_attn_pipe: ALL nkv heads in one call. pp = nw handles from sme_pipe_new (pp[0]'s stream is
+ * used; nw, nh are ignored), Q fp32 [nkv][NR][HD] unscaled, K/V at key 0 of head 0 (head h at +h*hb), rs, hb, is_q8,
+ * nkv, nk, scale; O [nkv][NR][HD], m, l [nkv][NR]. */
+void sme_attn_pipe(void ** pp, int nw, int nh, const float * Q, const uint8_t * K, const uint8_t * V, size_t rs,
+                   size_t hb, int is_q8, int nkv, int nk, float scale, float * O, float * m, float * l);
+
+/* ---------------------------------------------------------------- extensions of the reference ABI */
+
+/* Last error of the calling thread ("" if none). No counterpart in the reference (its C ABI has no error channel). */
+const char * pa_hip_last_error(void);
+
+/* Rows per KV head and head dim the sme_* entry points assume (default 48 and 256 = phone-attn.h:78-79). hd must be
+ * 128 or 256. Returns 0, or -1 for an unsupported shape. Process-wide; set it before the first call. */
+int pa_hip_set_compat_shape(int nr, int hd);
+
+/* Release a handle from sme_ws_new / sme_pipe_new (the reference never frees them). */
+void pa_hip_ws_free(void * w);
+
+/* ---------------------------------------------------------------- 2. device-resident engine path */
+
+enum { PA_FMT_F16 = 0, PA_FMT_Q8_0 = 1, PA_FMT_Q4_0 = 2 };   /* config_req.is_q8 (phone-attn.h:15, 88) */
+enum { PA_QMODE_GGML = 0,  /* Q -> q8_0 per 32-block like ggml's CPU flash_attn_ext (K's vec_dot type), s = dot*scale */
+       PA_QMODE_F16 = 1 }; /* Q -> f16(q*scale) like the reference engines (phone-attn.h:595-599, sme_attn.c:276-280) */
+
+typedef struct pa_hip_shape {
+    uint32_t nkv;     /* KV heads per row (config_req.n_head_kv) */
+    uint32_t rows;    /* query rows per KV head: 48 at the reference shape, 8*n_tok at GQA 8 */
+    uint32_t hd;      /* head dim: 128 or 256 */
+    uint32_t fmt;     /* PA_FMT_* */
+    uint32_t rs;      /* bytes per key row, all heads (config_req.rs) */
+    uint32_t hb;      /* bytes per head inside a row (config_req.hb) */
+    uint32_t qmode;   /* PA_QMODE_* */
+    float scale;      /* softmax scale */
+} pa_hip_shape;
+
+/* A workspace: split-K partials and the prepared Q, grown on demand with hipMalloc. Calls that share a workspace must
+ * be ordered (same stream, or synchronised); use one workspace per concurrent stream. */
+typedef struct pa_hip_ws pa_hip_ws;
+pa_hip_ws * pa_hip_ws_new(int device);
+void pa_hip_ws_destroy(pa_hip_ws * ws);
+
+/* engine::alloc_page / free_page (phone-attn.h:168-169): K and V storage of one page in HBM (device pointers, 256-byte
+ * aligned). Returns 0 or -1. */
+int pa_hip_alloc_page(size_t bytes, void ** k, void ** v);
+void pa_hip_free_page(void * k, void * v);
+
+/* The partial attention of one call: n_pages pages, page i holds nkeys[i] keys of rows rs bytes at k_pages[i] /
+ * v_pages[i] (device pointers; the host arrays themselves are read during the call only). Q, O, m, l are device
+ * pointers laid out as in the header comment. Enqueued on `stream` (a hipStream_t; NULL = the null stream); returns
+ * 0 once enqueued, -1 on a bad argument (nothing enqueued, pa_hip_last_error() says why). */
+int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * shape, const void * const * k_pages, const void * const * v_pages,
+                const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, void * stream);
+
+/* Greedy acceptance of a draft block (no code in the reference tree: the fork's LLAMA_BATCHED_ARGMAX, serve.sh:8-9, 281):
+ * logits fp32 [n_rows][vocab] and draft int32 [n_rows-1] on the device. out (device int32 [2 + n_rows]) receives
+ * out[0] = k, the length of the longest prefix with argmax(logits[i]) == draft[i]; out[1] = the bonus token
+ * argmax(logits[k]); out[2+i] = argmax(logits[i]) with the lowest index on ties (the first NaN wins, as numpy.argmax).
+ * n_rows <= 64. Returns 0 once enqueued, -1 on a bad argument. */
+int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, int64_t vocab, const int32_t * draft, int32_t * out,
+                  void * stream);
+
+/* Measurement hook, no counterpart in the reference: the next pa_hip_attn call on this workspace records ev_start
+ * (a hipEvent_t) just before its attention kernel and ev_end just after it, on the call's stream, so a caller can time
+ * that kernel alone with hipEventElapsedTime. One call consumes the pair. Returns 0. */
+int pa_hip_ws_time_next(pa_hip_ws * ws, void * ev_start, void * ev_end);
+
+/* q8_0 / q4_0 quantizer of the library (ggml quantize_row_q8_0_ref / q4_0_ref semantics; the q8_0 one prepares Q in
+ * PA_QMODE_GGML): n fp32 values (multiple of 32) at x -> blocks at y, both device pointers. Returns 0 or -1. */
+int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream);
+
+#ifdef __cplusplus
+}
+#endif

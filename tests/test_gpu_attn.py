@@ -1,0 +1,134 @@
+"""GPU parity of the device engine path (pa_hip_attn, through the C ABI) against the CPU oracle on the same bytes.
+
+Tolerance (written here): 2e-3 relative on O (per row, after rebasing to the oracle's max), on m
+(relative to max(1, |m|)) and on l, against the ggml-faithful restatement (orc_attn_ggml) in PA_QMODE_GGML, and against
+the fp64 closed form with the reference engines' rounding (f16(q*scale)) in PA_QMODE_F16."""
+import os
+
+import numpy as np
+import pytest
+
+import backburner_amd as bb
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def ws():
+    w = bb.Workspace()
+    yield w
+    w.close()
+
+
+def case(fmt, nkv, rows, hd, nk, seed, rs_pad=0, k_amp=1.0, outliers=0):
+    hb = orc.head_bytes(fmt, hd)
+    rs = nkv * hb + rs_pad
+    K = orc.fill_rows(seed, fmt, nkv, hd, nk, rs=rs, amp=k_amp, n_outliers=outliers, outlier_mul=8.0)
+    V = orc.fill_rows(seed + 1, fmt, nkv, hd, nk, rs=rs)
+    Q = orc.normal(seed + 2, 0, nkv * rows * hd).reshape(nkv * rows, hd)
+    return K, V, Q, rs
+
+
+def run_and_check(ws, fmt, nkv, rows, hd, nk, seed, qmode=bb.QMODE_GGML, page_keys=bb.PAGE, rs_pad=0, k_amp=1.0, outliers=0,
+                  tol=TOL):
+    print(f"case fmt={fmt} nkv={nkv} rows={rows} hd={hd} nk={nk} qmode={qmode} pages={page_keys}", flush=True)
+    K, V, Q, rs = case(fmt, nkv, rows, hd, nk, seed, rs_pad, k_amp, outliers)
+    shape = bb.make_shape(nkv, rows, hd, fmt, qmode, rs=rs)
+    O, m, l = bb.attn_host(shape, K, V, Q, page_keys=page_keys, ws=ws)
+    if qmode == bb.QMODE_GGML:
+        ref = orc.attn_ggml(orc.make_shape(nkv, rows, hd, fmt, orc.QMODE_GGML, rs=rs), Q, K, V, nk)
+    else:
+        ref = orc.attn_exact(orc.make_shape(nkv, rows, hd, fmt, orc.QMODE_F16, rs=rs), Q, K, V, nk)
+    eo, em, el = orc.rel_err(O, m, l, *ref)
+    assert eo < tol and em < tol and el < tol, (eo, em, el)
+    return eo, em, el
+
+
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16])
+@pytest.mark.parametrize("rows", [8, 48, 128, 300])
+@pytest.mark.parametrize("hd", [128, 256])
+def test_parity_ggml(ws, fmt, rows, hd):
+    run_and_check(ws, fmt, 2, rows, hd, 1000, seed=100 + rows + hd + fmt, page_keys=512)
+
+
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16])
+@pytest.mark.parametrize("rows", [8, 48])
+def test_parity_reference_rounding(ws, fmt, rows):
+    run_and_check(ws, fmt, 4, rows, 256, 700, seed=7 + rows + fmt, qmode=bb.QMODE_F16, page_keys=256)
+
+
+def test_outlier_channels_and_padding(ws):
+    """K with 4 x8 outlier channels per head (the long-context decode configuration) and rows padded past nkv*hb."""
+    run_and_check(ws, bb.FMT_Q8_0, 8, 8, 128, 2048, seed=31, rs_pad=16, outliers=4)
+
+
+@pytest.mark.parametrize("pages", [[3, 0, 64, 1, 130], [1], [4096, 4096, 17], [10] * 70])
+def test_ragged_pages(ws, pages):
+    """Uneven page sizes, empty pages, single keys and more pages than one launch holds (70 > 64)."""
+    run_and_check(ws, bb.FMT_Q8_0, 2, 8, 128, sum(pages), seed=5 + len(pages), page_keys=pages)
+
+
+@pytest.mark.parametrize("rows", [8, 128, 512])
+def test_empty(ws, rows):
+    shape = bb.make_shape(2, rows, 128, bb.FMT_Q8_0)
+    Q = orc.normal(1, 0, 2 * rows * 128).reshape(2 * rows, 128)
+    O, m, l = bb.attn_host(shape, np.zeros(0, np.uint8), np.zeros(0, np.uint8), Q, page_keys=[], ws=ws)
+    assert np.all(O == 0) and np.all(np.isneginf(m)) and np.all(l == 0)
+
+
+def test_chunking_invariance(ws):
+    """Split-K chunking and the merge must not change the result beyond fp32 reordering."""
+    K, V, Q, rs = case(bb.FMT_Q8_0, 2, 8, 128, 5000, 77)
+    shape = bb.make_shape(2, 8, 128, bb.FMT_Q8_0, rs=rs)
+    outs = []
+    for chunk in ("64", "1024", "4096", "8192"):
+        os.environ["PA_HIP_CHUNK"] = chunk
+        try:
+            outs.append(bb.attn_host(shape, K, V, Q, page_keys=1500, ws=ws))
+        finally:
+            del os.environ["PA_HIP_CHUNK"]
+    for O, m, l in outs[1:]:
+        eo, em, el = orc.rel_err(O, m, l, *outs[0])
+        assert eo < 1e-5 and em < 1e-6 and el < 1e-5, (eo, em, el)
+
+
+def test_bad_arguments(ws):
+    with pytest.raises(bb.PaHipError, match="hd must be"):
+        bb.attn_host(bb.make_shape(1, 8, 64, bb.FMT_Q8_0), np.zeros(68, np.uint8), np.zeros(68, np.uint8),
+                     np.zeros((8, 64), np.float32), page_keys=[1], ws=ws)
+    s = bb.make_shape(2, 8, 128, bb.FMT_Q8_0)
+    s.rs = 100
+    with pytest.raises(bb.PaHipError, match="too small"):
+        bb.attn_host(s, np.zeros(100, np.uint8), np.zeros(100, np.uint8), np.zeros((16, 128), np.float32), page_keys=[1], ws=ws)
+
+
+def test_decode_128k_full_size(ws):
+    """The long-context decode layer at full size (131,072 q8_0 keys, 8 KV heads, GQA 8, outlier channels): GPU-made
+    pages downloaded and checked against the oracle on the same bytes."""
+    nkv, rows, hd, nk = 8, 8, 128, 131072
+    hb = bb.head_bytes(bb.FMT_Q8_0, hd)
+    rs = nkv * hb
+    syn = bb.synth()
+    kbuf, vbuf = bb.DeviceBuffer(nk * rs), bb.DeviceBuffer(nk * rs)
+    ch = orc.outlier_channels(1001, nkv, hd, 4)
+    dch = bb.DeviceBuffer.from_array(ch)
+    assert syn.pa_synth_fill_rows(kbuf.ptr, 1, nkv, hd, rs, 0, nk, 1001, 1.0, 4, dch.ptr, 8.0, None) == 0
+    assert syn.pa_synth_fill_rows(vbuf.ptr, 1, nkv, hd, rs, 0, nk, 1002, 1.0, 0, None, 1.0, None) == 0
+    bb.device_sync()
+    Q = orc.normal(1003, 0, nkv * rows * hd).reshape(nkv * rows, hd)
+    pages = bb.Pages([kbuf.ptr + i * 4096 * rs for i in range(32)], [vbuf.ptr + i * 4096 * rs for i in range(32)], [4096] * 32, [])
+    dq = bb.DeviceBuffer.from_array(Q)
+    do, dml = bb.DeviceBuffer(nkv * rows * hd * 4), bb.DeviceBuffer(nkv * rows * 8)
+    shape = bb.make_shape(nkv, rows, hd, bb.FMT_Q8_0)
+    ws.attn(shape, pages, dq.ptr, do.ptr, dml.ptr, dml.ptr + nkv * rows * 4)
+    bb.device_sync()
+    O = do.download(np.float32).reshape(-1, hd)
+    ml = dml.download(np.float32)
+    K = kbuf.download(np.uint8)
+    V = vbuf.download(np.uint8)
+    ref = orc.attn_ggml(orc.make_shape(nkv, rows, hd, orc.Q8_0), Q, K, V, nk)
+    eo, em, el = orc.rel_err(O, ml[:nkv * rows], ml[nkv * rows:], *ref)
+    print("decode 128k parity", eo, em, el)
+    assert eo < TOL and em < TOL and el < TOL, (eo, em, el)

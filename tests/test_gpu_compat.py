@@ -1,0 +1,91 @@
+"""GPU: the reference's C ABI exported by libpa_hip.so (sme_attn_partial / sme_attn_pipe, phone-attn.h:63-71) with host
+buffers at the reference shape (48 rows per KV head, head dim 256), and the reference's own pa-tool, compiled unchanged
+and linked against libpa_hip.so, running its loopback fp64 check on the GPU engine."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import backburner_amd as bb
+import oracle as orc
+from tests.test_ref_patool import check_line, run_patool
+
+pytestmark = pytest.mark.gpu
+ROOT = Path(__file__).resolve().parents[1]
+TOOL_HIP = ROOT / "oracle" / "_ref" / "pa-tool-hip"
+NR, HD = 48, 256
+
+
+@pytest.fixture(scope="module", autouse=True)
+def shape():
+    bb.set_compat_shape(NR, HD)
+
+
+def ref_case(fmt, nkv, nk, seed):
+    hb = orc.head_bytes(fmt, HD)
+    rs = nkv * hb
+    K = orc.fill_rows(seed, fmt, nkv, HD, nk, rs=rs, amp=1.5)
+    V = orc.fill_rows(seed + 1, fmt, nkv, HD, nk, rs=rs)
+    Q = (orc.normal(seed + 2, 0, nkv * NR * HD) * 1.7).astype(np.float32).reshape(nkv * NR, HD)
+    return K, V, Q, rs, hb
+
+
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_F16])
+def test_sme_attn_partial_per_head(fmt):
+    assert bb.sme2_available() == 1
+    nkv, nk = 4, 4096
+    K, V, Q, rs, hb = ref_case(fmt, nkv, nk, 11 + fmt)
+    w = bb.sme_ws_new()
+    O = np.zeros((nkv * NR, HD), np.float32); m = np.zeros(nkv * NR, np.float32); l = np.zeros(nkv * NR, np.float32)
+    for h in range(nkv):
+        bb.sme_attn_partial(w, Q[h * NR:], HD, K, V, rs, fmt, nk, 1.0 / 16, 512, O[h * NR:], m[h * NR:], l[h * NR:], k_off=h * hb)
+    ref = orc.attn_exact(orc.make_shape(nkv, NR, HD, fmt, orc.QMODE_F16, scale=1.0 / 16, rs=rs), Q, K, V, nk)
+    eo, em, el = orc.rel_err(O, m, l, *ref)
+    assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
+
+
+def test_sme_attn_pipe_all_heads_and_empty():
+    nkv, nk = 4, 4160
+    K, V, Q, rs, hb = ref_case(bb.FMT_Q8_0, nkv, nk, 21)
+    pp = [bb.sme_pipe_new(1)]
+    O = np.zeros((nkv * NR, HD), np.float32); m = np.zeros(nkv * NR, np.float32); l = np.zeros(nkv * NR, np.float32)
+    bb.sme_attn_pipe(pp, Q, K, V, rs, hb, 1, nkv, nk, 1.0 / 16, O, m, l)
+    ref = orc.attn_exact(orc.make_shape(nkv, NR, HD, orc.Q8_0, orc.QMODE_F16, scale=1.0 / 16, rs=rs), Q, K, V, nk)
+    eo, em, el = orc.rel_err(O, m, l, *ref)
+    assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
+    bb.sme_attn_pipe(pp, Q, K, V, rs, hb, 1, nkv, 0, 1.0 / 16, O, m, l)   # sme_attn.c:281: empty -> m = -1e30, l = 0
+    assert np.all(O == 0) and np.all(m == np.float32(-1e30)) and np.all(l == 0)
+
+
+def test_sme_attn_pipe_device_pages():
+    """Pages already in HBM (pa_hip_alloc_page memory) are read in place."""
+    nkv, nk = 2, 1000
+    K, V, Q, rs, hb = ref_case(bb.FMT_Q8_0, nkv, nk, 31)
+    dk, dv = bb.DeviceBuffer.from_array(K), bb.DeviceBuffer.from_array(V)
+    import ctypes as C
+    O = np.zeros((nkv * NR, HD), np.float32); m = np.zeros(nkv * NR, np.float32); l = np.zeros(nkv * NR, np.float32)
+    arr = (C.c_void_p * 1)(bb.sme_pipe_new(1))
+    bb.lib().sme_attn_pipe(arr, 1, 1, bb._fp(Q), dk.ptr, dv.ptr, rs, hb, 1, nkv, nk, 1.0 / 16, bb._fp(O), bb._fp(m), bb._fp(l))
+    ref = orc.attn_exact(orc.make_shape(nkv, NR, HD, orc.Q8_0, orc.QMODE_F16, scale=1.0 / 16, rs=rs), Q, K, V, nk)
+    eo, em, el = orc.rel_err(O, m, l, *ref)
+    assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
+
+
+needs_tool = pytest.mark.skipif(not TOOL_HIP.exists(), reason="oracle/_ref/pa-tool-hip not built (reference checkout absent at build time)")
+
+
+@needs_tool
+@pytest.mark.parametrize("nkeys,ntok", [(8192, 8), (4096, 1)])
+def test_reference_patool_on_gpu_engine(nkeys, ntok):
+    """pa-tool serve (its C-ABI engine = libpa_hip.so) + pa-tool test: the reference's fp64 gate (5e-3)."""
+    out = run_patool(TOOL_HIP, [nkeys, 3, 2], {"PA_NTOK": ntok})
+    eo, el, verdict = check_line(out)
+    print(out)
+    assert verdict == "PASS" and eo < 2e-3 and el < 2e-3, out
+
+
+@needs_tool
+def test_reference_patool_big_on_gpu_engine():
+    out = run_patool(TOOL_HIP, [4096, 2, 2], {"PA_BIG_TOK": 16})
+    assert re.search(r"big vs one-group calls: .* -> PASS", out), out
