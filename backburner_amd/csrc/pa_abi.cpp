@@ -140,8 +140,8 @@ int pick_cfg(uint32_t rows, uint32_t hd) {
     const int forced = env_int("PA_HIP_CFG", -1);
     if (forced >= 0 && forced <= CFG_PREFILL) return forced;
     if (rows <= 16) return CFG_DECODE;
-    if (rows <= 64) return CFG_MID;
-    if (rows <= 128 || hd == 256) return CFG_VERIFY;
+    if (rows <= 64 || hd == 256) return CFG_MID;
+    if (rows <= 128) return CFG_VERIFY;
     return CFG_PREFILL;
 }
 
@@ -202,7 +202,8 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
     }
 
     // buffers
-    const size_t q16_b = (size_t) s->nkv * qr * s->hd * sizeof(_Float16);
+    const size_t q16_n = (size_t) s->nkv * qr * s->hd;
+    const size_t q16_b = 2 * q16_n * sizeof(_Float16);
     const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
     const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
     if (!ensure(ws->q16, ws->q16_cap, q16_b, "hipMalloc q16") || !ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") ||
@@ -211,7 +212,8 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
 
     // Q -> fp16 rows (q8_0-rounded in ggml mode)
     QprepArgs qa;
-    qa.q = Q; qa.q16 = ws->q16; qa.nkv = s->nkv; qa.rows = s->rows; qa.qr = qr; qa.hd = s->hd; qa.qmode = s->qmode; qa.scale = s->scale;
+    qa.q = Q; qa.q16 = ws->q16; qa.q16_lo = (uint32_t) q16_n; qa.nkv = s->nkv; qa.rows = s->rows; qa.qr = qr; qa.hd = s->hd;
+    qa.qmode = s->qmode; qa.fmt = s->fmt; qa.scale = s->scale;
     if (!hip_ok(launch_qprep(qa, st), "qprep launch")) return -1;
 
     const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
@@ -232,7 +234,8 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         a.n_items = ln.n_chunks * units;
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
         a.s_mul = (s->qmode == PA_QMODE_GGML ? s->scale : 1.0f) * 1.4426950408889634f;
-        a.q16 = ws->q16; a.po = ws->po; a.pml = ws->pml;
+        a.q16 = ws->q16; a.q16_lo = (uint32_t) q16_n; a.hilo = (s->qmode == PA_QMODE_GGML && s->fmt != PA_FMT_F16) ? 1u : 0u;
+        a.po = ws->po; a.pml = ws->pml;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
         if (!hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch")) return -1;
     }

@@ -7,7 +7,7 @@ namespace pa_hip {
 
 constexpr int MAXP = 64;   // pages per attention launch (more are split over several launches into one slot array)
 
-enum { CFG_DECODE = 0, CFG_MID = 1, CFG_VERIFY = 2, CFG_PREFILL = 3 };   // 16 / 64 / 128 / 256 (hd 256: 128) rows per workgroup
+enum { CFG_DECODE = 0, CFG_MID = 1, CFG_VERIFY = 2, CFG_PREFILL = 3 };   // 16 / 64 / 128 / 128 rows per workgroup
 
 struct AttnArgs {
     const uint8_t * kp[MAXP];       // page base (key 0, head 0) of K / V
@@ -19,8 +19,10 @@ struct AttnArgs {
     uint32_t qr;                    // padded rows per KV head in q16 / the slots
     uint32_t nrb;                   // row blocks per KV head
     uint32_t slot0;                 // slot of chunk 0 of this launch
-    float s_mul;                    // factor from the fp16 dot to base-2 logits
-    const _Float16 * q16;           // [nkv][qr][hd]
+    float s_mul;                    // factor from the dot to base-2 logits (scale * log2 e, or log2 e)
+    uint32_t hilo;                  // 1: the query's lo half is non-zero (ggml mode, quantized K)
+    uint32_t q16_lo;                // offset of the lo half from q16 (elements)
+    const _Float16 * q16;           // hi [nkv][qr][hd], lo at q16 + q16_lo
     float * po;                     // [slot][nkv][qr][hd]
     float2 * pml;                   // [slot][nkv][qr]: (max in base-2 units, sum)
 };
@@ -34,8 +36,9 @@ struct MergeArgs {
 
 struct QprepArgs {
     const float * q;                // [nkv][rows][hd] fp32
-    _Float16 * q16;                 // [nkv][qr][hd]
-    uint32_t nkv, rows, qr, hd, qmode;
+    _Float16 * q16;                 // hi [nkv][qr][hd], lo at q16 + q16_lo
+    uint32_t q16_lo;
+    uint32_t nkv, rows, qr, hd, qmode, fmt;
     float scale;
 };
 

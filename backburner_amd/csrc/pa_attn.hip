@@ -21,8 +21,10 @@ namespace pa_hip {
 
 // ---------------------------------------------------------------- tile loaders (HBM -> registers -> LDS fp16)
 template <int HD, int FMT, int NB, int NT>
-__device__ __forceinline__ void load_k_tile(_Float16 * __restrict__ Ks, const uint8_t * __restrict__ kb, uint32_t rs,
-                                            uint32_t jt, int nvalid, int tid) {
+__device__ __forceinline__ void load_k_tile(_Float16 * __restrict__ Ks, float * __restrict__ Ksc, const uint8_t * __restrict__ kb,
+                                            uint32_t rs, uint32_t jt, int nvalid, int tid, float s_mul) {
+    // K stays exact: the quants (q8_0: q, q4_0: nib - 8) as integer-valued fp16, and d * s_mul per (block, key) in
+    // Ksc[blk][key], applied to each block's fp32 partial dot after the MFMA (the order ggml's q8_0 x q8_0 dot uses).
     constexpr int NBLK = HD / 32, KS = HD + 8;
     #pragma unroll
     for (int it0 = 0; it0 < NB * NBLK; it0 += NT) {
@@ -30,41 +32,39 @@ __device__ __forceinline__ void load_k_tile(_Float16 * __restrict__ Ks, const ui
         if (NB * NBLK % NT != 0 && it >= NB * NBLK) break;
         const int key = it / NBLK, blk = it % NBLK;
         pa_u4 o[4] = {};
+        float sc = 0.0f;
         if (key < nvalid) {
             const uint8_t * src = kb + (size_t) (jt + key) * rs;
             if constexpr (FMT == 1) {
                 src += blk * 34;
-                const uint16_t db = pa_ld<uint16_t>(src);
+                sc = pa_f16_bits_to_f32(pa_ld<uint16_t>(src)) * s_mul;
                 const pa_u4 q0 = pa_ld<pa_u4>(src + 2), q1 = pa_ld<pa_u4>(src + 18);
-                const _Float16 d = __builtin_bit_cast(_Float16, db);
-                const pa_h2 d2 = {d, d};
                 const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
                 #pragma unroll
                 for (int w = 0; w < 8; w++) {
                     uint32_t lo, hi;
-                    pa_deq_q8x4(qw[w], d2, lo, hi);
+                    pa_int_q8x4(qw[w], lo, hi);
                     o[w / 2][(w % 2) * 2 + 0] = lo;
                     o[w / 2][(w % 2) * 2 + 1] = hi;
                 }
             } else if constexpr (FMT == 2) {
                 src += blk * 18;
-                const uint16_t db = pa_ld<uint16_t>(src);
+                sc = pa_f16_bits_to_f32(pa_ld<uint16_t>(src)) * s_mul;
                 const pa_u4 q = pa_ld<pa_u4>(src + 2);
-                const _Float16 d = __builtin_bit_cast(_Float16, db);
-                const pa_h2 d2 = {d, d};
                 const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
                 #pragma unroll
                 for (int w = 0; w < 4; w++) {   // bytes 4w..4w+3: low nibbles = elements 4w.., high = 16+4w..
                     uint32_t lo, hi;
-                    pa_deq_nib4(qw[w] & 0x0f0f0f0fu, d2, lo, hi);
+                    pa_int_nib4(qw[w] & 0x0f0f0f0fu, lo, hi);
                     o[w / 2][(w % 2) * 2 + 0] = lo;
                     o[w / 2][(w % 2) * 2 + 1] = hi;
-                    pa_deq_nib4((qw[w] >> 4) & 0x0f0f0f0fu, d2, lo, hi);
+                    pa_int_nib4((qw[w] >> 4) & 0x0f0f0f0fu, lo, hi);
                     o[2 + w / 2][(w % 2) * 2 + 0] = lo;
                     o[2 + w / 2][(w % 2) * 2 + 1] = hi;
                 }
             } else {
                 src += blk * 64;
+                sc = s_mul;
                 #pragma unroll
                 for (int c = 0; c < 4; c++) o[c] = pa_ld<pa_u4>(src + 16 * c);
             }
@@ -72,6 +72,7 @@ __device__ __forceinline__ void load_k_tile(_Float16 * __restrict__ Ks, const ui
         pa_u4 * dst = (pa_u4 *) (Ks + key * KS + blk * 32);
         #pragma unroll
         for (int c = 0; c < 4; c++) dst[c] = o[c];
+        Ksc[blk * NB + key] = sc;
     }
 }
 
@@ -148,12 +149,13 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     constexpr int KPW = NB / WK;       // keys of a tile per wave
     static_assert(KPW % 32 == 0, "each wave needs whole 32-key steps");
     constexpr int ROWS_WG = 16 * RT * WR;
-    constexpr int TILE_LDS = (NB * KS + HD * VS) * 2;
+    constexpr int TILE_LDS = (NB * KS + HD * VS) * 2 + NKD * NB * 4;
     constexpr int COMB_LDS = WK > 1 ? WK * ROWS_WG * (HD + 2) * 4 : 0;
     constexpr int LDS = TILE_LDS > COMB_LDS ? TILE_LDS : COMB_LDS;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
     _Float16 * Ks = (_Float16 *) smem;
     _Float16 * Vt = Ks + NB * KS;
+    float * Ksc = (float *) (Vt + HD * VS);   // [NKD][NB]: K block scale * s_mul
 
     // ---- which (chunk, head, row block). Items are numbered chunk-major (row block fastest) and XCD x (= blockIdx % 8 in
     // the dispatch order) takes the contiguous item range [x*T8, (x+1)*T8): the heads of one chunk (which share cache
@@ -171,14 +173,19 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     const int wr = wave % WR, wk = wave / WR, g = lane / 16, n = lane % 16;
     const uint32_t row_base = rb * ROWS_WG + wr * RT * 16;   // first row of this wave's row tiles (within the head)
 
-    // ---- Q^T fragments (B operand of QK): lane (g, n) holds row n, dims 32kd + 8g .. +7
-    pa_h8 qf[RT][NKD];
+    // ---- Q^T fragments (B operand of QK): lane (g, n) holds row n, dims 32kd + 8g .. +7, as hi + lo fp16 pairs whose sum
+    // is the prepared query exactly (q8_0-rounded in ggml mode); lo is all zero when a.hilo == 0
+    pa_h8 qh[RT][NKD], ql[RT][NKD];
     #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        const _Float16 * qrow = a.q16 + ((size_t) h * a.qr + row_base + rt * 16 + n) * HD + 8 * g;
+        const size_t off = ((size_t) h * a.qr + row_base + rt * 16 + n) * HD + 8 * g;
         #pragma unroll
-        for (int kd = 0; kd < NKD; kd++) qf[rt][kd] = *(const pa_h8 *) (qrow + 32 * kd);
+        for (int kd = 0; kd < NKD; kd++) {
+            qh[rt][kd] = *(const pa_h8 *) (a.q16 + off + 32 * kd);
+            ql[rt][kd] = *(const pa_h8 *) (a.q16 + a.q16_lo + off + 32 * kd);
+        }
     }
+    const bool hilo = a.hilo != 0;
     pa_f4 o[RT][ND];
     float mrow[RT], lrow[RT];
     #pragma unroll
@@ -196,14 +203,15 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
       for (uint32_t jt = j0; jt < j1; jt += NB) {
         const int nvalid = (int) min((uint32_t) NB, j1 - jt);
         __syncthreads();
-        load_k_tile<HD, FMT, NB, NT>(Ks, kb, a.rs, jt, nvalid, tid);
+        load_k_tile<HD, FMT, NB, NT>(Ks, Ksc, kb, a.rs, jt, nvalid, tid, s_mul);
         load_v_tile<HD, FMT, NB, NT>(Vt, vb, a.rs, jt, nvalid, tid);
         __syncthreads();
         #pragma unroll
         for (int ks = 0; ks < KPW / 32; ks++) {
             const int kbase = wk * KPW + ks * 32;                 // first key of this 32-key step within the tile
             if (kbase >= nvalid) break;
-            // S^T = K . Q^T for two 16-key subtiles
+            // S^T = K . Q^T for two 16-key subtiles, one MFMA (two with the lo half) per 32-dim block: exact integer-scaled
+            // partial dots, combined in fp32 with the block's K scale (already times s_mul: base-2 logits come out)
             pa_f4 s[RT][2];
             #pragma unroll
             for (int rt = 0; rt < RT; rt++) s[rt][0] = s[rt][1] = (pa_f4){0.f, 0.f, 0.f, 0.f};
@@ -211,10 +219,19 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
             for (int kd = 0; kd < NKD; kd++) {
                 const pa_h8 k0 = *(const pa_h8 *) (Ks + (kbase + n) * KS + 32 * kd + 8 * g);
                 const pa_h8 k1 = *(const pa_h8 *) (Ks + (kbase + 16 + n) * KS + 32 * kd + 8 * g);
+                const pa_f4 d0 = *(const pa_f4 *) (Ksc + kd * NB + kbase + 4 * g);
+                const pa_f4 d1 = *(const pa_f4 *) (Ksc + kd * NB + kbase + 16 + 4 * g);
                 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
-                    s[rt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qf[rt][kd], s[rt][0], 0, 0, 0);
-                    s[rt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qf[rt][kd], s[rt][1], 0, 0, 0);
+                    const pa_f4 z = {0.f, 0.f, 0.f, 0.f};
+                    pa_f4 a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[rt][kd], z, 0, 0, 0);
+                    pa_f4 a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[rt][kd], z, 0, 0, 0);
+                    if (hilo) {
+                        a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, ql[rt][kd], a0, 0, 0, 0);
+                        a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, ql[rt][kd], a1, 0, 0, 0);
+                    }
+                    s[rt][0] += d0 * a0;
+                    s[rt][1] += d1 * a1;
                 }
             }
             // V^T operand: lane (g, n) = dim 16*db + n, keys kbase + 4g..+3 and kbase + 16 + 4g..+3
@@ -225,8 +242,8 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
                 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int k0i = kbase + 4 * g + i, k1i = kbase + 16 + 4 * g + i;
-                    v[i] = k0i < nvalid ? s[rt][0][i] * s_mul : -INFINITY;
-                    v[4 + i] = k1i < nvalid ? s[rt][1][i] * s_mul : -INFINITY;
+                    v[i] = k0i < nvalid ? s[rt][0][i] : -INFINITY;
+                    v[4 + i] = k1i < nvalid ? s[rt][1][i] : -INFINITY;
                 }
                 float tm = v[0];
                 #pragma unroll
@@ -343,26 +360,36 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
 }
 
 // ---------------------------------------------------------------- Q preparation
-// One thread per (row, 32-block): Q fp32 [nkv][rows][HD] -> Q16 [nkv][qr][HD] (rows >= `rows` zero).
-// PA_QMODE_GGML: q8_0 of the block (d = amax/127, id = 1/d, q = roundf(x*id), d -> fp16: quantize_row_q8_0_ref),
-// then the fp16 value f16(d16 * q); the softmax scale is applied to the fp32 dot. PA_QMODE_F16: f16(x*scale).
+// One thread per (row, 32-block): Q fp32 [nkv][rows][HD] -> hi [nkv][qr][HD] and lo (at +q16_lo) fp16 with hi + lo equal to
+// the query value the dot product must see (rows >= `rows` zero).
+// PA_QMODE_GGML, quantized K: q8_0 of the block (d = amax/127, id = 1/d, q = roundf(x*id), d -> fp16:
+// quantize_row_q8_0_ref), value t = d16 * q (exact in fp32), hi = f16(t), lo = f16(t - hi) - exact, so the fp16 MFMA
+// against integer K reproduces ggml's integer block dot. PA_QMODE_GGML, f16 K: f16(x) (ggml's vec_dot_type for f16 K).
+// PA_QMODE_F16: f16(x*scale) (the reference engines). lo = 0 in the last two.
 __global__ __launch_bounds__(256) void qprep_kernel(const QprepArgs a) {
     const uint32_t nblk = a.hd / 32;
     const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= a.nkv * a.qr * nblk) return;
     const uint32_t blk = idx % nblk, row = (idx / nblk) % a.qr, h = idx / nblk / a.qr;
-    _Float16 * dst = a.q16 + ((size_t) h * a.qr + row) * a.hd + blk * 32;
-    if (row >= a.rows) { for (int j = 0; j < 32; j++) dst[j] = (_Float16) 0.0f; return; }
+    const size_t off = ((size_t) h * a.qr + row) * a.hd + blk * 32;
+    _Float16 * hi = a.q16 + off, * lo = a.q16 + a.q16_lo + off;
+    if (row >= a.rows) { for (int j = 0; j < 32; j++) hi[j] = lo[j] = (_Float16) 0.0f; return; }
     const float * x = a.q + ((size_t) h * a.rows + row) * a.hd + blk * 32;
-    if (a.qmode == 0) {
+    if (a.qmode == 0 && a.fmt != 0) {
         float amax = 0.0f;
         for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const float d16 = (float) (_Float16) d;
-        for (int j = 0; j < 32; j++) dst[j] = (_Float16) (d16 * roundf(x[j] * id));
+        for (int j = 0; j < 32; j++) {
+            const float t = d16 * roundf(x[j] * id);
+            const _Float16 th = (_Float16) t;
+            hi[j] = th;
+            lo[j] = (_Float16) (t - (float) th);
+        }
     } else {
-        for (int j = 0; j < 32; j++) dst[j] = (_Float16) (x[j] * a.scale);
+        const float mul = a.qmode == 0 ? 1.0f : a.scale;
+        for (int j = 0; j < 32; j++) { hi[j] = (_Float16) (x[j] * mul); lo[j] = (_Float16) 0.0f; }
     }
 }
 
@@ -406,13 +433,15 @@ static hipError_t launch_attn(const AttnArgs & a, uint32_t grid, hipStream_t st)
 
 template <int HD, int FMT>
 static hipError_t launch_attn_cfg(int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st) {
-    switch (cfg) {
-        case CFG_DECODE:  return launch_attn<HD, FMT, 1, 1, 2, 64>(a, grid, st);
-        case CFG_MID:     return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
-        case CFG_VERIFY:  return launch_attn<HD, FMT, 2, 4, 1, 64>(a, grid, st);
-        case CFG_PREFILL: if constexpr (HD == 128) return launch_attn<HD, FMT, 4, 4, 1, 64>(a, grid, st);
-                          else return launch_attn<HD, FMT, 2, 4, 1, 64>(a, grid, st);
-        default: return hipErrorInvalidValue;
+    if constexpr (HD == 256) {   // head dim 256 (the reference shape): at most 64 rows per workgroup (registers)
+        if (cfg == CFG_DECODE) return launch_attn<HD, FMT, 1, 1, 2, 64>(a, grid, st);
+        return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
+    } else {
+        switch (cfg) {
+            case CFG_DECODE: return launch_attn<HD, FMT, 1, 1, 2, 64>(a, grid, st);
+            case CFG_MID:    return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
+            default:         return launch_attn<HD, FMT, 2, 4, 1, 64>(a, grid, st);   // verify / prefill
+        }
     }
 }
 
@@ -431,12 +460,9 @@ hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32
 
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
     nb = 64;
-    switch (cfg) {
-        case CFG_DECODE: rows_per_wg = 16; break;
-        case CFG_MID: rows_per_wg = 64; break;
-        case CFG_VERIFY: rows_per_wg = 128; break;
-        default: rows_per_wg = hd == 128 ? 256 : 128; break;
-    }
+    if (cfg == CFG_DECODE) rows_per_wg = 16;
+    else if (cfg == CFG_MID || hd == 256) rows_per_wg = 64;
+    else rows_per_wg = 128;
 }
 
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {

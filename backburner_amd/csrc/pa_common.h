@@ -19,20 +19,19 @@ __device__ __forceinline__ uint32_t pa_as_u32(pa_h2 h) { return __builtin_bit_ca
 // v_perm_b32: byte k of the result = selector byte k; 0-3 pick bytes of `lo`, 4-7 bytes of `hi`, 12 = 0x00.
 __device__ __forceinline__ uint32_t pa_perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 
-// Four int8 (a dword of q8_0 quants) -> four fp16 d*q, in two packed halves (elements 0,1 and 2,3).
-// Bias trick: q ^ 0x80 is q + 128 as an unsigned byte; 0x64XX as fp16 is 1024 + XX; minus 1152 gives q exactly, and the
-// one rounding is the multiply by d (the same f16(d*q) the reference kernels produce, pa-metal.mm:398).
-__device__ __forceinline__ void pa_deq_q8x4(uint32_t q, pa_h2 d2, uint32_t & lo, uint32_t & hi) {
+// Four int8 (a dword of q8_0 quants) -> four integer-valued fp16 q (exact), in two packed halves (elements 0,1 and 2,3).
+// Bias trick: q ^ 0x80 is q + 128 as an unsigned byte; 0x64XX as fp16 is 1024 + XX; minus 1152 gives q exactly.
+__device__ __forceinline__ void pa_int_q8x4(uint32_t q, uint32_t & lo, uint32_t & hi) {
     const uint32_t x = q ^ 0x80808080u;
     const pa_h2 bias = {(_Float16) 1152.0f, (_Float16) 1152.0f};
-    lo = pa_as_u32((pa_as_h2(pa_perm(0x64646464u, x, 0x04010400u)) - bias) * d2);
-    hi = pa_as_u32((pa_as_h2(pa_perm(0x64646464u, x, 0x04030402u)) - bias) * d2);
+    lo = pa_as_u32(pa_as_h2(pa_perm(0x64646464u, x, 0x04010400u)) - bias);
+    hi = pa_as_u32(pa_as_h2(pa_perm(0x64646464u, x, 0x04030402u)) - bias);
 }
-// Four 4-bit values (low nibbles of a dword, already masked to 0x0f0f0f0f) -> fp16 d*(nib-8).
-__device__ __forceinline__ void pa_deq_nib4(uint32_t n, pa_h2 d2, uint32_t & lo, uint32_t & hi) {
+// Four 4-bit values (masked to 0x0f0f0f0f) -> four integer-valued fp16 nib - 8 (exact).
+__device__ __forceinline__ void pa_int_nib4(uint32_t n, uint32_t & lo, uint32_t & hi) {
     const pa_h2 bias = {(_Float16) 1032.0f, (_Float16) 1032.0f};
-    lo = pa_as_u32((pa_as_h2(pa_perm(0x64646464u, n, 0x04010400u)) - bias) * d2);
-    hi = pa_as_u32((pa_as_h2(pa_perm(0x64646464u, n, 0x04030402u)) - bias) * d2);
+    lo = pa_as_u32(pa_as_h2(pa_perm(0x64646464u, n, 0x04010400u)) - bias);
+    hi = pa_as_u32(pa_as_h2(pa_perm(0x64646464u, n, 0x04030402u)) - bias);
 }
 // Byte e of two dwords (two keys, same element) -> packed fp16 pair (key0, key1) of the biased value 1024 + byte.
 __device__ __forceinline__ uint32_t pa_pair_byte(uint32_t x1, uint32_t x0, int e) {
