@@ -57,7 +57,7 @@ def build(verbose: bool = False) -> None:
     for lib, srcs in LIBS.items():
         objs = [str(BUILD / (s + ".o")) for s in srcs]
         tmp = PKG / (lib + ".tmp")
-        _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
+        _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", f"-Wl,-soname,{lib}", *objs, "-o", str(tmp)], verbose)
         os.replace(tmp, PKG / lib)
     # the oracle (test infrastructure) and, where the reference checkout exists, its pa-tool builds
     _run(["make", "-s", "-C", str(ROOT / "oracle")], verbose)

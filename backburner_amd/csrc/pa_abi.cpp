@@ -74,8 +74,8 @@ int env_int(const char * name, int def) { const char * e = getenv(name); return 
 // ---------------------------------------------------------------- the workspace
 struct pa_hip_ws {
     int device = 0;
-    _Float16 * q16 = nullptr; size_t q16_cap = 0;
     float * po = nullptr; size_t po_cap = 0;
+    unsigned int * ctr = nullptr; size_t ctr_cap = 0;
     float2 * pml = nullptr; size_t pml_cap = 0;
     unsigned long long * apart = nullptr; size_t apart_cap = 0;
     unsigned int * acount = nullptr;
@@ -105,7 +105,7 @@ extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
 extern "C" void pa_hip_ws_destroy(pa_hip_ws * w) {
     if (!w) return;
     (void) hipDeviceSynchronize();
-    hipFree(w->q16); hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
+    hipFree(w->ctr); hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
     hipFree(w->dk); hipFree(w->dv); hipFree(w->dq); hipFree(w->dout);
     if (w->stream) hipStreamDestroy(w->stream);
     delete w;
@@ -177,9 +177,9 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
     const uint32_t nrb = (s->rows + rows_wg - 1) / rows_wg, qr = nrb * rows_wg;
     const uint32_t units = s->nkv * nrb;
 
-    // split-K chunking per launch (pages go in groups of MAXP): aim at ~4 workgroups per CU for the memory-bound shapes
-    // and one per CU for the row-heavy ones; a chunk is a multiple of the key tile
-    const int target = env_int("PA_HIP_TARGET_WG", cfg == CFG_DECODE || cfg == CFG_MID ? 1024 : cfg == CFG_VERIFY ? 768 : 256);
+    // split-K chunking per launch (pages go in groups of MAXP): about one workgroup per CU (PA_HIP_TARGET_WG), a chunk a
+    // multiple of the key tile; a chunk may span pages
+    const int target = env_int("PA_HIP_TARGET_WG", 256);
     const int forced_chunk = env_int("PA_HIP_CHUNK", 0);
     struct launch_t { int p0, np; uint32_t keys, chunk, n_chunks, slot0; };
     std::vector<launch_t> L;
@@ -200,25 +200,28 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         L.push_back({p0, np, keys, chunk, nch, n_slots});
         n_slots += nch;
     }
+    const bool fused = L.size() <= 1;   // one launch: its last workgroups fold the slots; else a separate merge kernel
 
-    // buffers
-    const size_t q16_n = (size_t) s->nkv * qr * s->hd;
-    const size_t q16_b = 2 * q16_n * sizeof(_Float16);
+    // buffers: split-K slots and the fold counters
     const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
     const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
-    if (!ensure(ws->q16, ws->q16_cap, q16_b, "hipMalloc q16") || !ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") ||
-        !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
+    if (!ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") || !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
         return -1;
-
-    // Q -> fp16 rows (q8_0-rounded in ggml mode)
-    QprepArgs qa;
-    qa.q = Q; qa.q16 = ws->q16; qa.q16_lo = (uint32_t) q16_n; qa.nkv = s->nkv; qa.rows = s->rows; qa.qr = qr; qa.hd = s->hd;
-    qa.qmode = s->qmode; qa.fmt = s->fmt; qa.scale = s->scale;
-    if (!hip_ok(launch_qprep(qa, st), "qprep launch")) return -1;
+    if ((size_t) units * sizeof(unsigned int) > ws->ctr_cap) {
+        if (!ensure(ws->ctr, ws->ctr_cap, std::max<size_t>(units * sizeof(unsigned int), 4096), "hipMalloc counters") ||
+            !hip_ok(hipMemset(ws->ctr, 0, ws->ctr_cap), "hipMemset counters"))   // once per growth; kernels keep them zero
+            return -1;
+    }
 
     const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
     ws->ev0 = ws->ev1 = nullptr;
     if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
+    if (L.empty()) {   // no keys: the fold of zero slots writes (0, -inf, 0)
+        MergeArgs ma;
+        ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
+        ma.n_slots = 0; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
+    }
     for (const launch_t & ln : L) {
         AttnArgs a;
         std::memset(&a, 0, sizeof a);
@@ -233,18 +236,19 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.chunk;
         a.n_items = ln.n_chunks * units;
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
+        a.qmode = s->qmode; a.fused = fused ? 1u : 0u; a.scale = s->scale;
         a.s_mul = (s->qmode == PA_QMODE_GGML ? s->scale : 1.0f) * 1.4426950408889634f;
-        a.q16 = ws->q16; a.q16_lo = (uint32_t) q16_n; a.hilo = (s->qmode == PA_QMODE_GGML && s->fmt != PA_FMT_F16) ? 1u : 0u;
-        a.po = ws->po; a.pml = ws->pml;
+        a.q = Q; a.po = ws->po; a.pml = ws->pml; a.counters = ws->ctr; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
         if (!hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch")) return -1;
     }
+    if (!fused) {
+        MergeArgs ma;
+        ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
+        ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
+    }
     if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
-
-    MergeArgs ma;
-    ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
-    ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
-    if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
     return 0;
 }
 

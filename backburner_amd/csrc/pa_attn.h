@@ -16,15 +16,18 @@ struct AttnArgs {
     uint32_t n_pages, n_chunks, chunk, n_items;   // chunk = keys per workgroup; n_items = chunks x heads x row blocks
     uint32_t rs, hb, nkv;
     uint32_t rows;                  // real query rows per KV head
-    uint32_t qr;                    // padded rows per KV head in q16 / the slots
+    uint32_t qr;                    // padded rows per KV head in the slots
     uint32_t nrb;                   // row blocks per KV head
     uint32_t slot0;                 // slot of chunk 0 of this launch
+    uint32_t qmode;                 // PA_QMODE_GGML / PA_QMODE_F16
+    uint32_t fused;                 // 1: this launch holds every chunk; the last workgroup per (head, row block) folds
+    float scale;                    // softmax scale (PA_QMODE_F16 folds it into Q)
     float s_mul;                    // factor from the dot to base-2 logits (scale * log2 e, or log2 e)
-    uint32_t hilo;                  // 1: the query's lo half is non-zero (ggml mode, quantized K)
-    uint32_t q16_lo;                // offset of the lo half from q16 (elements)
-    const _Float16 * q16;           // hi [nkv][qr][hd], lo at q16 + q16_lo
-    float * po;                     // [slot][nkv][qr][hd]
+    const float * q;                // [nkv][rows][hd] fp32
+    float * po;                     // slots [slot][nkv][qr][hd]
     float2 * pml;                   // [slot][nkv][qr]: (max in base-2 units, sum)
+    unsigned int * counters;        // [nkv][nrb], zero between calls
+    float * O, * m, * l;            // final [nkv][rows][hd], [nkv][rows]
 };
 
 struct MergeArgs {
@@ -34,17 +37,8 @@ struct MergeArgs {
     uint32_t n_slots, nkv, qr, rows;
 };
 
-struct QprepArgs {
-    const float * q;                // [nkv][rows][hd] fp32
-    _Float16 * q16;                 // hi [nkv][qr][hd], lo at q16 + q16_lo
-    uint32_t q16_lo;
-    uint32_t nkv, rows, qr, hd, qmode, fmt;
-    float scale;
-};
-
 hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st);
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st);
-hipError_t launch_qprep(const QprepArgs & a, hipStream_t st);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb);
 

@@ -1,15 +1,19 @@
 // pa_attn.hip - split-K partial attention over quantized K/V pages, fp16 MFMA (gfx950).
 //
-// One workgroup = one KV head x one block of 16*RT*WR query rows x one chunk of keys of one page. Per tile of NB keys the
-// workgroup dequantizes K into LDS row-major (fp16, [key][dim]) and V transposed ([dim][key]) - the int8/int4 -> fp16
-// conversion runs once per tile and feeds every row of the block. Each wave then computes, per 32-key step,
-//   S^T (keys x rows) = K . Q^T with v_mfma_f32_16x16x32_f16 (A = K rows from LDS, B = Q^T held in registers),
-// which leaves lane (g, n) with row n's scores of keys 4g..4g+3 (+16): exactly the B operand of
+// One workgroup = one KV head x one block of 16*RT*WR query rows x one chunk of keys (a chunk may span pages). Per tile
+// of NB keys (inside one page) the workgroup stages K into LDS row-major as exact integer-valued fp16 (the q8_0/q4_0
+// quants) with the block scales in a small side array, and V transposed ([dim][key], fp16 d*q). The next tile's raw
+// bytes are already in flight into registers while the current tile is computed. Each wave then computes, per 32-key
+// step,
+//   S^T (keys x rows) = K . Q^T with v_mfma_f32_16x16x32_f16, one MFMA per 32-dim block (= one quant block), and the
+//   block's partial dot times d_k * scale * log2 e added in fp32 - the query is q8_0-rounded in-kernel (ggml's Q
+//   handling) and held as an exact fp16 hi + lo pair, so the QK dot equals ggml's integer block dot;
 //   O^T (dims x rows) += V^T . P^T,
-// so the probabilities never leave registers, and the running max / sum of row n live in the lanes that own row n.
-// Online softmax runs in base 2 (the softmax scale and log2 e are folded into one multiply). WK waves may split the
-// keys of a tile; their states are merged through LDS at the end. Each workgroup writes one split-K slot
-// (O^T unnormalised, m in base-2 units, l); pa_merge_kernel folds the slots.
+// so lane (g, n) holds row n's scores of keys 4g..4g+3 (+16) - exactly the B operand of the PV MFMA - and the running
+// max / sum of row n live in the lanes that own row n. Online softmax is in base 2. WK waves may split the keys of a
+// tile; their states merge through LDS. Each workgroup then writes one split-K slot (O^T unnormalised, base-2 max, sum);
+// the last workgroup of a (head, row block) to finish - a device-scope counter, no waiting - folds the slots into the
+// final (O, m, l). With one chunk the workgroup writes the final result directly.
 //
 // Reference roles: pa_attn_big + pa_big_load (pa-metal.mm:379-487: per (row tile, KV head, key chunk), dequant a K/V
 // block, S = QK^T, online softmax with key masking, O = alpha O + PV, write a slot) and pa_merge / pa_merge_big
@@ -19,125 +23,157 @@
 
 namespace pa_hip {
 
-// ---------------------------------------------------------------- tile loaders (HBM -> registers -> LDS fp16)
+// ---------------------------------------------------------------- raw tile registers
+// Words per 32-dim block item: q8_0 = fp16 scale + 32 bytes (9 dwords), q4_0 = scale + 16 bytes (5), f16 = 64 bytes (16).
+template <int FMT> struct ItemWords { static constexpr int W = FMT == 1 ? 9 : FMT == 2 ? 5 : 16; };
+
+template <int HD, int FMT, int NB, int NT> struct TileRegs {
+    static constexpr int NBLK = HD / 32, W = ItemWords<FMT>::W;
+    static constexpr int KIT = (NB * NBLK + NT - 1) / NT;        // K items (key, block) per thread
+    static constexpr int VIT = (NB / 2 * NBLK + NT - 1) / NT;    // V items (key pair, block) per thread
+    uint32_t k[KIT][W];
+    uint32_t v[VIT][2][W];
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_item(uint32_t * w, const uint8_t * row, int blk) {
+    if constexpr (FMT == 1) {
+        const uint8_t * s = row + blk * 34;
+        w[0] = pa_ld<uint16_t>(s);
+        const pa_u4 a = pa_ld<pa_u4>(s + 2), b = pa_ld<pa_u4>(s + 18);
+        w[1] = a.x; w[2] = a.y; w[3] = a.z; w[4] = a.w; w[5] = b.x; w[6] = b.y; w[7] = b.z; w[8] = b.w;
+    } else if constexpr (FMT == 2) {
+        const uint8_t * s = row + blk * 18;
+        w[0] = pa_ld<uint16_t>(s);
+        const pa_u4 a = pa_ld<pa_u4>(s + 2);
+        w[1] = a.x; w[2] = a.y; w[3] = a.z; w[4] = a.w;
+    } else {
+        const uint8_t * s = row + blk * 64;
+        #pragma unroll
+        for (int c = 0; c < 4; c++) { const pa_u4 a = pa_ld<pa_u4>(s + 16 * c); w[4 * c] = a.x; w[4 * c + 1] = a.y; w[4 * c + 2] = a.z; w[4 * c + 3] = a.w; }
+    }
+}
+
+// HBM -> registers for the tile of keys [jt, jt + nvalid) of one page (keys past nvalid read nothing, hold zeros)
 template <int HD, int FMT, int NB, int NT>
-__device__ __forceinline__ void load_k_tile(_Float16 * __restrict__ Ks, float * __restrict__ Ksc, const uint8_t * __restrict__ kb,
-                                            uint32_t rs, uint32_t jt, int nvalid, int tid, float s_mul) {
-    // K stays exact: the quants (q8_0: q, q4_0: nib - 8) as integer-valued fp16, and d * s_mul per (block, key) in
-    // Ksc[blk][key], applied to each block's fp32 partial dot after the MFMA (the order ggml's q8_0 x q8_0 dot uses).
-    constexpr int NBLK = HD / 32, KS = HD + 8;
+__device__ __forceinline__ void load_tile(TileRegs<HD, FMT, NB, NT> & R, const uint8_t * __restrict__ kb, const uint8_t * __restrict__ vb,
+                                          uint32_t rs, uint32_t jt, int nvalid, int tid) {
+    using T = TileRegs<HD, FMT, NB, NT>;
     #pragma unroll
-    for (int it0 = 0; it0 < NB * NBLK; it0 += NT) {
-        const int it = it0 + tid;
-        if (NB * NBLK % NT != 0 && it >= NB * NBLK) break;
-        const int key = it / NBLK, blk = it % NBLK;
-        pa_u4 o[4] = {};
-        float sc = 0.0f;
-        if (key < nvalid) {
-            const uint8_t * src = kb + (size_t) (jt + key) * rs;
-            if constexpr (FMT == 1) {
-                src += blk * 34;
-                sc = pa_f16_bits_to_f32(pa_ld<uint16_t>(src)) * s_mul;
-                const pa_u4 q0 = pa_ld<pa_u4>(src + 2), q1 = pa_ld<pa_u4>(src + 18);
-                const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-                #pragma unroll
-                for (int w = 0; w < 8; w++) {
-                    uint32_t lo, hi;
-                    pa_int_q8x4(qw[w], lo, hi);
-                    o[w / 2][(w % 2) * 2 + 0] = lo;
-                    o[w / 2][(w % 2) * 2 + 1] = hi;
-                }
-            } else if constexpr (FMT == 2) {
-                src += blk * 18;
-                sc = pa_f16_bits_to_f32(pa_ld<uint16_t>(src)) * s_mul;
-                const pa_u4 q = pa_ld<pa_u4>(src + 2);
-                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-                #pragma unroll
-                for (int w = 0; w < 4; w++) {   // bytes 4w..4w+3: low nibbles = elements 4w.., high = 16+4w..
-                    uint32_t lo, hi;
-                    pa_int_nib4(qw[w] & 0x0f0f0f0fu, lo, hi);
-                    o[w / 2][(w % 2) * 2 + 0] = lo;
-                    o[w / 2][(w % 2) * 2 + 1] = hi;
-                    pa_int_nib4((qw[w] >> 4) & 0x0f0f0f0fu, lo, hi);
-                    o[2 + w / 2][(w % 2) * 2 + 0] = lo;
-                    o[2 + w / 2][(w % 2) * 2 + 1] = hi;
-                }
-            } else {
-                src += blk * 64;
-                sc = s_mul;
-                #pragma unroll
-                for (int c = 0; c < 4; c++) o[c] = pa_ld<pa_u4>(src + 16 * c);
+    for (int i = 0; i < T::KIT; i++) {
+        const int it = i * NT + tid, key = it / T::NBLK, blk = it % T::NBLK;
+        #pragma unroll
+        for (int x = 0; x < T::W; x++) R.k[i][x] = 0;
+        if (it < NB * T::NBLK && key < nvalid) load_item<FMT>(R.k[i], kb + (size_t) (jt + key) * rs, blk);
+    }
+    #pragma unroll
+    for (int i = 0; i < T::VIT; i++) {
+        const int it = i * NT + tid, kp = it / T::NBLK, blk = it % T::NBLK;
+        #pragma unroll
+        for (int x = 0; x < T::W; x++) R.v[i][0][x] = R.v[i][1][x] = 0;
+        if (it < NB / 2 * T::NBLK) {
+            if (2 * kp < nvalid) load_item<FMT>(R.v[i][0], vb + (size_t) (jt + 2 * kp) * rs, blk);
+            if (2 * kp + 1 < nvalid) load_item<FMT>(R.v[i][1], vb + (size_t) (jt + 2 * kp + 1) * rs, blk);
+        }
+    }
+}
+
+// registers -> LDS: K as exact integer-valued fp16 + Ksc[blk][key] = d * s_mul; V transposed Vt[dim][key] = f16(d*q),
+// written as (key pair) dwords. A zero-filled item (past nvalid) writes zeros and a zero scale.
+template <int HD, int FMT, int NB, int NT>
+__device__ __forceinline__ void store_tile(const TileRegs<HD, FMT, NB, NT> & R, _Float16 * __restrict__ Ks, float * __restrict__ Ksc,
+                                           _Float16 * __restrict__ Vt, int tid, float s_mul) {
+    using T = TileRegs<HD, FMT, NB, NT>;
+    constexpr int KS = HD + 8, VS = NB + 4;
+    #pragma unroll
+    for (int i = 0; i < T::KIT; i++) {
+        const int it = i * NT + tid, key = it / T::NBLK, blk = it % T::NBLK;
+        if (it >= NB * T::NBLK) break;
+        const uint32_t * w = R.k[i];
+        pa_u4 o[4];
+        float sc;
+        if constexpr (FMT == 1) {
+            sc = pa_f16_bits_to_f32((uint16_t) w[0]) * s_mul;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) {
+                uint32_t lo, hi;
+                pa_int_q8x4(w[1 + q], lo, hi);
+                o[q / 2][(q % 2) * 2 + 0] = lo;
+                o[q / 2][(q % 2) * 2 + 1] = hi;
             }
+        } else if constexpr (FMT == 2) {
+            sc = pa_f16_bits_to_f32((uint16_t) w[0]) * s_mul;
+            #pragma unroll
+            for (int q = 0; q < 4; q++) {   // bytes 4q..4q+3: low nibbles = elements 4q.., high nibbles = 16 + 4q..
+                uint32_t lo, hi;
+                pa_int_nib4(w[1 + q] & 0x0f0f0f0fu, lo, hi);
+                o[q / 2][(q % 2) * 2 + 0] = lo;
+                o[q / 2][(q % 2) * 2 + 1] = hi;
+                pa_int_nib4((w[1 + q] >> 4) & 0x0f0f0f0fu, lo, hi);
+                o[2 + q / 2][(q % 2) * 2 + 0] = lo;
+                o[2 + q / 2][(q % 2) * 2 + 1] = hi;
+            }
+        } else {
+            sc = s_mul;
+            #pragma unroll
+            for (int c = 0; c < 4; c++) o[c] = (pa_u4){w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
         }
         pa_u4 * dst = (pa_u4 *) (Ks + key * KS + blk * 32);
         #pragma unroll
         for (int c = 0; c < 4; c++) dst[c] = o[c];
         Ksc[blk * NB + key] = sc;
     }
-}
-
-// V tile, transposed: Vt[dim][key] (row stride NB+4 halves). A work item is (key pair, 32-dim block): the two keys'
-// values of one dim are packed into one dword, so the LDS writes are 4-byte and the PV operand reads 8-byte runs of keys.
-template <int HD, int FMT, int NB, int NT>
-__device__ __forceinline__ void load_v_tile(_Float16 * __restrict__ Vt, const uint8_t * __restrict__ vb, uint32_t rs,
-                                            uint32_t jt, int nvalid, int tid) {
-    constexpr int NBLK = HD / 32, VS = NB + 4;
-    constexpr int NIT = NB / 2 * NBLK;
     #pragma unroll
-    for (int it0 = 0; it0 < NIT; it0 += NT) {
-        const int it = it0 + tid;
-        if (NIT % NT != 0 && it >= NIT) break;
-        const int kp = it / NBLK, blk = it % NBLK, k0 = 2 * kp;
+    for (int i = 0; i < T::VIT; i++) {
+        const int it = i * NT + tid, kp = it / T::NBLK, blk = it % T::NBLK, k0 = 2 * kp;
+        if (it >= NB / 2 * T::NBLK) break;
+        const uint32_t * a = R.v[i][0], * b = R.v[i][1];
         uint32_t * col = (uint32_t *) (Vt + (blk * 32) * VS + k0);   // dim blk*32 + d at col + d*VS/2
-        const bool v0 = k0 < nvalid, v1 = k0 + 1 < nvalid;
-        const uint8_t * s0 = vb + (size_t) (jt + k0) * rs, * s1 = s0 + rs;
         if constexpr (FMT == 1) {
-            pa_u4 a0 = {}, a1 = {}, b0 = {}, b1 = {};
-            uint16_t da = 0, dbb = 0;
-            if (v0) { s0 += blk * 34; da = pa_ld<uint16_t>(s0); a0 = pa_ld<pa_u4>(s0 + 2); a1 = pa_ld<pa_u4>(s0 + 18); }
-            if (v1) { s1 += blk * 34; dbb = pa_ld<uint16_t>(s1); b0 = pa_ld<pa_u4>(s1 + 2); b1 = pa_ld<pa_u4>(s1 + 18); }
-            const pa_h2 d2 = {__builtin_bit_cast(_Float16, da), __builtin_bit_cast(_Float16, dbb)};
+            const pa_h2 d2 = {__builtin_bit_cast(_Float16, (uint16_t) a[0]), __builtin_bit_cast(_Float16, (uint16_t) b[0])};
             const pa_h2 bias = {(_Float16) 1152.0f, (_Float16) 1152.0f};
-            const uint32_t xa[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            const uint32_t xb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
             #pragma unroll
-            for (int w = 0; w < 8; w++) {
-                const uint32_t x0 = xa[w] ^ 0x80808080u, x1 = xb[w] ^ 0x80808080u;
+            for (int q = 0; q < 8; q++) {
+                const uint32_t x0 = a[1 + q] ^ 0x80808080u, x1 = b[1 + q] ^ 0x80808080u;
                 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    col[(4 * w + e) * (VS / 2)] = pa_as_u32((pa_as_h2(pa_pair_byte(x1, x0, e)) - bias) * d2);
+                for (int e = 0; e < 4; e++) col[(4 * q + e) * (VS / 2)] = pa_as_u32((pa_as_h2(pa_pair_byte(x1, x0, e)) - bias) * d2);
             }
         } else if constexpr (FMT == 2) {
-            pa_u4 a = {}, b = {};
-            uint16_t da = 0, dbb = 0;
-            if (v0) { s0 += blk * 18; da = pa_ld<uint16_t>(s0); a = pa_ld<pa_u4>(s0 + 2); }
-            if (v1) { s1 += blk * 18; dbb = pa_ld<uint16_t>(s1); b = pa_ld<pa_u4>(s1 + 2); }
-            const pa_h2 d2 = {__builtin_bit_cast(_Float16, da), __builtin_bit_cast(_Float16, dbb)};
+            const pa_h2 d2 = {__builtin_bit_cast(_Float16, (uint16_t) a[0]), __builtin_bit_cast(_Float16, (uint16_t) b[0])};
             const pa_h2 bias = {(_Float16) 1032.0f, (_Float16) 1032.0f};
-            const uint32_t xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
             #pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const uint32_t l0 = xa[w] & 0x0f0f0f0fu, l1 = xb[w] & 0x0f0f0f0fu;
-                const uint32_t h0 = (xa[w] >> 4) & 0x0f0f0f0fu, h1 = (xb[w] >> 4) & 0x0f0f0f0fu;
+            for (int q = 0; q < 4; q++) {
+                const uint32_t l0 = a[1 + q] & 0x0f0f0f0fu, l1 = b[1 + q] & 0x0f0f0f0fu;
+                const uint32_t h0 = (a[1 + q] >> 4) & 0x0f0f0f0fu, h1 = (b[1 + q] >> 4) & 0x0f0f0f0fu;
                 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    col[(4 * w + e) * (VS / 2)] = pa_as_u32((pa_as_h2(pa_pair_byte(l1, l0, e)) - bias) * d2);
-                    col[(16 + 4 * w + e) * (VS / 2)] = pa_as_u32((pa_as_h2(pa_pair_byte(h1, h0, e)) - bias) * d2);
+                    col[(4 * q + e) * (VS / 2)] = pa_as_u32((pa_as_h2(pa_pair_byte(l1, l0, e)) - bias) * d2);
+                    col[(16 + 4 * q + e) * (VS / 2)] = pa_as_u32((pa_as_h2(pa_pair_byte(h1, h0, e)) - bias) * d2);
                 }
             }
         } else {
-            pa_u4 a[4] = {}, b[4] = {};
-            if (v0) { s0 += blk * 64; for (int c = 0; c < 4; c++) a[c] = pa_ld<pa_u4>(s0 + 16 * c); }
-            if (v1) { s1 += blk * 64; for (int c = 0; c < 4; c++) b[c] = pa_ld<pa_u4>(s1 + 16 * c); }
             #pragma unroll
-            for (int w = 0; w < 16; w++) {   // dword w = dims 2w, 2w+1
-                const uint32_t x0 = a[w / 4][w % 4], x1 = b[w / 4][w % 4];
-                col[(2 * w) * (VS / 2)] = pa_perm(x1, x0, 0x05040100u);
-                col[(2 * w + 1) * (VS / 2)] = pa_perm(x1, x0, 0x07060302u);
+            for (int q = 0; q < 16; q++) {   // dword q = dims 2q, 2q+1
+                col[(2 * q) * (VS / 2)] = pa_perm(b[q], a[q], 0x05040100u);
+                col[(2 * q + 1) * (VS / 2)] = pa_perm(b[q], a[q], 0x07060302u);
             }
         }
     }
 }
+
+// ---------------------------------------------------------------- tiles of a chunk, page by page
+struct TileIt {
+    uint32_t p, jt, j1;   // page, first key of the tile in the page, end of the chunk's part of the page
+    // from page p on: the first page that holds keys of [key_lo, key_hi), and its key range in page coordinates
+    __device__ __forceinline__ void settle(const AttnArgs & a, uint32_t key_lo, uint32_t key_hi) {
+        while (p < a.n_pages && (a.pstart[p + 1] <= key_lo || a.pstart[p + 1] == a.pstart[p])) p++;
+        if (p < a.n_pages) {
+            jt = max(key_lo, a.pstart[p]) - a.pstart[p];
+            j1 = min(key_hi, a.pstart[p + 1]) - a.pstart[p];
+        }
+    }
+    __device__ __forceinline__ bool valid(const AttnArgs & a, uint32_t key_hi) const { return p < a.n_pages && a.pstart[p] + jt < key_hi; }
+};
 
 // ---------------------------------------------------------------- the attention kernel
 template <int HD, int FMT, int RT, int WR, int WK, int NB>
@@ -145,7 +181,7 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     constexpr int NT = 64 * WR * WK;
     constexpr int KS = HD + 8, VS = NB + 4;
     constexpr int ND = HD / 16;        // 16-dim blocks of O^T
-    constexpr int NKD = HD / 32;       // 32-dim k-steps of QK
+    constexpr int NKD = HD / 32;       // 32-dim blocks (= quant blocks) of QK
     constexpr int KPW = NB / WK;       // keys of a tile per wave
     static_assert(KPW % 32 == 0, "each wave needs whole 32-key steps");
     constexpr int ROWS_WG = 16 * RT * WR;
@@ -153,6 +189,7 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     constexpr int COMB_LDS = WK > 1 ? WK * ROWS_WG * (HD + 2) * 4 : 0;
     constexpr int LDS = TILE_LDS > COMB_LDS ? TILE_LDS : COMB_LDS;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
+    __shared__ bool s_last;
     _Float16 * Ks = (_Float16 *) smem;
     _Float16 * Vt = Ks + NB * KS;
     float * Ksc = (float *) (Vt + HD * VS);   // [NKD][NB]: K block scale * s_mul
@@ -166,26 +203,58 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     if (local >= t8 || w >= a.n_items) return;
     const uint32_t rb = w % a.nrb, h = (w / a.nrb) % a.nkv, c = w / (a.nrb * a.nkv);
     const uint32_t key_lo = c * a.chunk, key_hi = min(a.pstart[a.n_pages], key_lo + a.chunk);
-    uint32_t p = 0;
-    while (p + 1 < a.n_pages && a.pstart[p + 1] <= key_lo) p++;
 
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wr = wave % WR, wk = wave / WR, g = lane / 16, n = lane % 16;
     const uint32_t row_base = rb * ROWS_WG + wr * RT * 16;   // first row of this wave's row tiles (within the head)
 
-    // ---- Q^T fragments (B operand of QK): lane (g, n) holds row n, dims 32kd + 8g .. +7, as hi + lo fp16 pairs whose sum
-    // is the prepared query exactly (q8_0-rounded in ggml mode); lo is all zero when a.hilo == 0
+    // ---- start the first tile's loads, then prepare Q while they fly
+    TileIt itr = {0, 0, 0};
+    itr.settle(a, key_lo, key_hi);
+    TileRegs<HD, FMT, NB, NT> R;
+    bool have = itr.valid(a, key_hi);
+    if (have) load_tile<HD, FMT, NB, NT>(R, a.kp[itr.p] + (size_t) h * a.hb, a.vp[itr.p] + (size_t) h * a.hb, a.rs, itr.jt,
+                                         (int) min((uint32_t) NB, itr.j1 - itr.jt), tid);
+
+    // Q^T fragments (B operand of QK): lane (g, n) holds row n, dims 32kd + 8g .. +7, as an fp16 hi + lo pair whose sum is
+    // exactly the value the dot product must see. ggml mode with quantized K: q8_0 of each 32-block (d = amax/127,
+    // id = 1/d, q = roundf(x*id), d -> fp16; quantize_row_q8_0_ref), value d16*q (exact in fp32), hi = f16, lo = f16(rest).
+    // ggml mode with f16 K: f16(x) (ggml's vec_dot_type for f16). PA_QMODE_F16: f16(x*scale) (the reference engines).
     pa_h8 qh[RT][NKD], ql[RT][NKD];
+    const bool qquant = a.qmode == 0 && FMT != 0;
     #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        const size_t off = ((size_t) h * a.qr + row_base + rt * 16 + n) * HD + 8 * g;
+        const uint32_t row = row_base + rt * 16 + n;
+        const bool live = row < a.rows;
+        const float * qrow = a.q + ((size_t) h * a.rows + (live ? row : 0)) * HD + 8 * g;
         #pragma unroll
         for (int kd = 0; kd < NKD; kd++) {
-            qh[rt][kd] = *(const pa_h8 *) (a.q16 + off + 32 * kd);
-            ql[rt][kd] = *(const pa_h8 *) (a.q16 + a.q16_lo + off + 32 * kd);
+            float x[8];
+            const pa_f4 x0 = live ? *(const pa_f4 *) (qrow + 32 * kd) : (pa_f4){0.f, 0.f, 0.f, 0.f};
+            const pa_f4 x1 = live ? *(const pa_f4 *) (qrow + 32 * kd + 4) : (pa_f4){0.f, 0.f, 0.f, 0.f};
+            x[0] = x0[0]; x[1] = x0[1]; x[2] = x0[2]; x[3] = x0[3]; x[4] = x1[0]; x[5] = x1[1]; x[6] = x1[2]; x[7] = x1[3];
+            if (qquant) {
+                float am = 0.0f;
+                #pragma unroll
+                for (int j = 0; j < 8; j++) am = fmaxf(am, fabsf(x[j]));
+                am = pa_wave_max16x4(am);                              // the block's 32 values sit in lanes n, n+16, n+32, n+48
+                const float d = am / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                const float d16 = (float) (_Float16) d;
+                #pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float t = d16 * roundf(x[j] * id);
+                    const _Float16 th = (_Float16) t;
+                    qh[rt][kd][j] = th;
+                    ql[rt][kd][j] = (_Float16) (t - (float) th);
+                }
+            } else {
+                const float mul = a.qmode == 0 ? 1.0f : a.scale;
+                #pragma unroll
+                for (int j = 0; j < 8; j++) { qh[rt][kd][j] = (_Float16) (x[j] * mul); ql[rt][kd][j] = (_Float16) 0.0f; }
+            }
         }
     }
-    const bool hilo = a.hilo != 0;
     pa_f4 o[RT][ND];
     float mrow[RT], lrow[RT];
     #pragma unroll
@@ -196,22 +265,23 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     }
     const float s_mul = a.s_mul;
 
-    for (; p < a.n_pages && a.pstart[p] < key_hi; p++) {
-      const uint32_t j0 = max(key_lo, a.pstart[p]) - a.pstart[p], j1 = min(key_hi, a.pstart[p + 1]) - a.pstart[p];
-      const uint8_t * kb = a.kp[p] + (size_t) h * a.hb;
-      const uint8_t * vb = a.vp[p] + (size_t) h * a.hb;
-      for (uint32_t jt = j0; jt < j1; jt += NB) {
-        const int nvalid = (int) min((uint32_t) NB, j1 - jt);
-        __syncthreads();
-        load_k_tile<HD, FMT, NB, NT>(Ks, Ksc, kb, a.rs, jt, nvalid, tid, s_mul);
-        load_v_tile<HD, FMT, NB, NT>(Vt, vb, a.rs, jt, nvalid, tid);
+    while (have) {
+        const int nvalid = (int) min((uint32_t) NB, itr.j1 - itr.jt);
+        __syncthreads();                                             // the previous tile's readers are done
+        store_tile<HD, FMT, NB, NT>(R, Ks, Ksc, Vt, tid, s_mul);
+        // next tile: its bytes fly while this one is computed
+        itr.jt += NB;
+        if (itr.jt >= itr.j1) { itr.p++; itr.settle(a, key_lo, key_hi); }
+        have = itr.valid(a, key_hi);
+        if (have) load_tile<HD, FMT, NB, NT>(R, a.kp[itr.p] + (size_t) h * a.hb, a.vp[itr.p] + (size_t) h * a.hb, a.rs, itr.jt,
+                                             (int) min((uint32_t) NB, itr.j1 - itr.jt), tid);
         __syncthreads();
         #pragma unroll
         for (int ks = 0; ks < KPW / 32; ks++) {
             const int kbase = wk * KPW + ks * 32;                 // first key of this 32-key step within the tile
             if (kbase >= nvalid) break;
-            // S^T = K . Q^T for two 16-key subtiles, one MFMA (two with the lo half) per 32-dim block: exact integer-scaled
-            // partial dots, combined in fp32 with the block's K scale (already times s_mul: base-2 logits come out)
+            // S^T = K . Q^T for two 16-key subtiles, one MFMA (two with the lo half) per 32-dim block: exact partial dots,
+            // combined in fp32 with the block's K scale (already times s_mul: base-2 logits come out)
             pa_f4 s[RT][2];
             #pragma unroll
             for (int rt = 0; rt < RT; rt++) s[rt][0] = s[rt][1] = (pa_f4){0.f, 0.f, 0.f, 0.f};
@@ -226,7 +296,7 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
                     const pa_f4 z = {0.f, 0.f, 0.f, 0.f};
                     pa_f4 a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[rt][kd], z, 0, 0, 0);
                     pa_f4 a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[rt][kd], z, 0, 0, 0);
-                    if (hilo) {
+                    if (qquant) {
                         a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, ql[rt][kd], a0, 0, 0, 0);
                         a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, ql[rt][kd], a1, 0, 0, 0);
                     }
@@ -234,16 +304,14 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
                     s[rt][1] += d1 * a1;
                 }
             }
-            // V^T operand: lane (g, n) = dim 16*db + n, keys kbase + 4g..+3 and kbase + 16 + 4g..+3
             pa_h8 pf[RT];
             #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
                 float v[8];
                 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int k0i = kbase + 4 * g + i, k1i = kbase + 16 + 4 * g + i;
-                    v[i] = k0i < nvalid ? s[rt][0][i] : -INFINITY;
-                    v[4 + i] = k1i < nvalid ? s[rt][1][i] : -INFINITY;
+                    v[i] = kbase + 4 * g + i < nvalid ? s[rt][0][i] : -INFINITY;
+                    v[4 + i] = kbase + 16 + 4 * g + i < nvalid ? s[rt][1][i] : -INFINITY;
                 }
                 float tm = v[0];
                 #pragma unroll
@@ -262,6 +330,7 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
                 #pragma unroll
                 for (int i = 0; i < 8; i++) pf[rt][i] = (_Float16) v[i];
             }
+            // O^T += V^T . P^T: lane (g, n) = dim 16*db + n, keys kbase + 4g..+3 and kbase + 16 + 4g..+3
             #pragma unroll
             for (int db = 0; db < ND; db++) {
                 const _Float16 * vr = Vt + (16 * db + n) * VS + kbase + 4 * g;
@@ -271,24 +340,35 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
                 for (int rt = 0; rt < RT; rt++) o[rt][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pf[rt], o[rt][db], 0, 0, 0);
             }
         }
-      }
     }
 
     // ---- per-row sums over the 4 lane groups
     #pragma unroll
     for (int rt = 0; rt < RT; rt++) lrow[rt] = pa_wave_sum16x4(lrow[rt]);
 
+    // ---- this workgroup's result: final (one chunk) or a split-K slot
+    const bool direct = a.n_chunks == 1 && a.fused;
     const uint32_t slot = a.slot0 + c;
     float * po = a.po + ((size_t) slot * a.nkv + h) * a.qr * HD;
     float2 * pml = a.pml + ((size_t) slot * a.nkv + h) * a.qr;
+    float * fO = a.O + (size_t) h * a.rows * HD;
+    float * fm = a.m + (size_t) h * a.rows, * fl = a.l + (size_t) h * a.rows;
+    auto emit = [&](uint32_t row, int d4, pa_f4 val, float M, float L) {
+        if (direct) {
+            *(pa_f4 *) (fO + (size_t) row * HD + 4 * d4) = val;
+            if (d4 == 0) { fm[row] = M == -INFINITY ? -INFINITY : M * PA_LN2; fl[row] = L; }
+        } else {
+            *(pa_f4 *) (po + (size_t) row * HD + 4 * d4) = val;
+            if (d4 == 0) pml[row] = make_float2(M, L);
+        }
+    };
     if constexpr (WK == 1) {
         #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const uint32_t row = row_base + rt * 16 + n;
             if (row >= a.rows) continue;
             #pragma unroll
-            for (int db = 0; db < ND; db++) *(pa_f4 *) (po + (size_t) row * HD + 16 * db + 4 * g) = o[rt][db];
-            if (g == 0) pml[row] = make_float2(mrow[rt], lrow[rt]);
+            for (int db = 0; db < ND; db++) emit(row, 4 * db + g, o[rt][db], mrow[rt], lrow[rt]);
         }
     } else {
         // merge the WK key-split states of the same rows through LDS
@@ -309,37 +389,100 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
             if (row >= a.rows) continue;
             float M = -INFINITY;
             #pragma unroll
-            for (int w = 0; w < WK; w++) M = fmaxf(M, cML[w * ROWS_WG + lr].x);
+            for (int q = 0; q < WK; q++) M = fmaxf(M, cML[q * ROWS_WG + lr].x);
             const float Ms = M == -INFINITY ? 0.0f : M;
             pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
             float L = 0.0f;
             #pragma unroll
-            for (int w = 0; w < WK; w++) {
-                const float2 ml = cML[w * ROWS_WG + lr];
+            for (int q = 0; q < WK; q++) {
+                const float2 ml = cML[q * ROWS_WG + lr];
                 const float wt = __builtin_amdgcn_exp2f(ml.x - Ms);
                 L += wt * ml.y;
-                acc += wt * *(const pa_f4 *) (cO + ((size_t) w * ROWS_WG + lr) * HD + 4 * d4);
+                acc += wt * *(const pa_f4 *) (cO + ((size_t) q * ROWS_WG + lr) * HD + 4 * d4);
             }
-            *(pa_f4 *) (po + (size_t) row * HD + 4 * d4) = acc;
-            if (d4 == 0) pml[row] = make_float2(M, L);
+            emit(row, d4, acc, M, L);
         }
     }
+    if (direct || !a.fused) return;
+
+    // ---- fused split-K fold: the last workgroup of this (head, row block) folds every slot
+    __threadfence();                                                  // publish this slot (device scope)
+    __syncthreads();
+    unsigned int * ctr = a.counters + h * a.nrb + rb;
+    if (tid == 0) {
+        const unsigned int done = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = done == a.n_chunks - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();                                                  // see every other slot
+    const size_t sstride = (size_t) a.nkv * a.qr;                    // rows between slots
+    const uint32_t r0 = rb * ROWS_WG, r1 = min(a.rows, r0 + ROWS_WG);
+    for (uint32_t e = tid; e < (r1 - r0) * (HD / 4); e += NT) {
+        const uint32_t row = r0 + e / (HD / 4), d4 = e % (HD / 4);
+        const float2 * ml = a.pml + (size_t) h * a.qr + row;
+        const float * op = a.po + ((size_t) h * a.qr + row) * HD + 4 * d4;
+        float M = -INFINITY;
+        uint32_t s = 0;
+        for (; s + 8 <= a.n_chunks; s += 8) {
+            float mm[8];
+            #pragma unroll
+            for (int q = 0; q < 8; q++) mm[q] = ml[(s + q) * sstride].x;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) M = fmaxf(M, mm[q]);
+        }
+        for (; s < a.n_chunks; s++) M = fmaxf(M, ml[s * sstride].x);
+        const float Ms = M == -INFINITY ? 0.0f : M;
+        pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
+        float L = 0.0f;
+        s = 0;
+        for (; s + 8 <= a.n_chunks; s += 8) {
+            float2 mlq[8];
+            pa_f4 oq[8];
+            #pragma unroll
+            for (int q = 0; q < 8; q++) { mlq[q] = ml[(s + q) * sstride]; oq[q] = *(const pa_f4 *) (op + (s + q) * sstride * HD); }
+            #pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float wt = __builtin_amdgcn_exp2f(mlq[q].x - Ms);   // an empty slot (-inf) weighs 0
+                L += wt * mlq[q].y;
+                acc += wt * oq[q];
+            }
+        }
+        for (; s < a.n_chunks; s++) {
+            const float2 mq = ml[s * sstride];
+            const float wt = __builtin_amdgcn_exp2f(mq.x - Ms);
+            L += wt * mq.y;
+            acc += wt * *(const pa_f4 *) (op + s * sstride * HD);
+        }
+        *(pa_f4 *) (fO + (size_t) row * HD + 4 * d4) = acc;
+        if (d4 == 0) { fm[row] = M == -INFINITY ? -INFINITY : M * PA_LN2; fl[row] = L; }
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next call
 }
 
-// ---------------------------------------------------------------- split-K fold
-// One workgroup per output row; thread t folds dims 4*(t % (HD/4)) over slots t / (HD/4), t / (HD/4) + SG, ...
+// ---------------------------------------------------------------- split-K fold as its own kernel
+// Used when one call needs several attention launches (more than MAXP pages). One workgroup per output row; thread t
+// folds dims 4*(t % (HD/4)) over slots t / (HD/4), t / (HD/4) + SG, ...
 template <int HD>
 __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     constexpr int TPR = HD / 4, SG = 256 / TPR;
     __shared__ pa_f4 red[SG][TPR];
     __shared__ float redl[SG];
+    __shared__ float redm[256];
     const uint32_t r = blockIdx.x;                   // output row = h*rows + i
     const uint32_t h = r / a.rows, i = r % a.rows;
     const int t = threadIdx.x, d4 = t % TPR, sg = t / TPR;
     const size_t stride = (size_t) a.nkv * a.qr;     // rows between slots
     const size_t pr = (size_t) h * a.qr + i;
     float M = -INFINITY;
-    for (uint32_t s = 0; s < a.n_slots; s++) M = fmaxf(M, a.pml[s * stride + pr].x);
+    for (uint32_t s = t; s < a.n_slots; s += 256) M = fmaxf(M, a.pml[s * stride + pr].x);
+    redm[t] = M;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (t < off) redm[t] = fmaxf(redm[t], redm[t + off]);
+        __syncthreads();
+    }
+    M = redm[0];
     const float Ms = M == -INFINITY ? 0.0f : M;
     pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
     float L = 0.0f;
@@ -359,42 +502,11 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     }
 }
 
-// ---------------------------------------------------------------- Q preparation
-// One thread per (row, 32-block): Q fp32 [nkv][rows][HD] -> hi [nkv][qr][HD] and lo (at +q16_lo) fp16 with hi + lo equal to
-// the query value the dot product must see (rows >= `rows` zero).
-// PA_QMODE_GGML, quantized K: q8_0 of the block (d = amax/127, id = 1/d, q = roundf(x*id), d -> fp16:
-// quantize_row_q8_0_ref), value t = d16 * q (exact in fp32), hi = f16(t), lo = f16(t - hi) - exact, so the fp16 MFMA
-// against integer K reproduces ggml's integer block dot. PA_QMODE_GGML, f16 K: f16(x) (ggml's vec_dot_type for f16 K).
-// PA_QMODE_F16: f16(x*scale) (the reference engines). lo = 0 in the last two.
-__global__ __launch_bounds__(256) void qprep_kernel(const QprepArgs a) {
-    const uint32_t nblk = a.hd / 32;
-    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= a.nkv * a.qr * nblk) return;
-    const uint32_t blk = idx % nblk, row = (idx / nblk) % a.qr, h = idx / nblk / a.qr;
-    const size_t off = ((size_t) h * a.qr + row) * a.hd + blk * 32;
-    _Float16 * hi = a.q16 + off, * lo = a.q16 + a.q16_lo + off;
-    if (row >= a.rows) { for (int j = 0; j < 32; j++) hi[j] = lo[j] = (_Float16) 0.0f; return; }
-    const float * x = a.q + ((size_t) h * a.rows + row) * a.hd + blk * 32;
-    if (a.qmode == 0 && a.fmt != 0) {
-        float amax = 0.0f;
-        for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        const float d16 = (float) (_Float16) d;
-        for (int j = 0; j < 32; j++) {
-            const float t = d16 * roundf(x[j] * id);
-            const _Float16 th = (_Float16) t;
-            hi[j] = th;
-            lo[j] = (_Float16) (t - (float) th);
-        }
-    } else {
-        const float mul = a.qmode == 0 ? 1.0f : a.scale;
-        for (int j = 0; j < 32; j++) { hi[j] = (_Float16) (x[j] * mul); lo[j] = (_Float16) 0.0f; }
-    }
-}
-
-// ggml quantize_row_q8_0_ref / quantize_row_q4_0_ref on the device, one thread per 32-block.
+// ---------------------------------------------------------------- device quantizers
+// ggml quantize_row_q8_0_ref / quantize_row_q4_0_ref, one thread per 32-block. Every float expression rounds as written
+// (no FMA contraction), as the oracle's C restatement does.
 __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, uint8_t * __restrict__ y, int64_t nblk, int fmt) {
+    #pragma clang fp contract(off)
     const int64_t b = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (b >= nblk) return;
     const float * xb = x + b * 32;
@@ -413,10 +525,13 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict_
         for (int j = 0; j < 32; j++) { const float v = xb[j]; if (amax < fabsf(v)) { amax = fabsf(v); mx = v; } }
         const float d = mx / -8.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        const uint16_t dh = __builtin_bit_cast(uint16_t, (_Float16) d);
+        // d = 0 / -8 is -0 (fp16 0x8000); keep the sign bit explicitly (a fused f32->f16 multiply-add would drop it)
+        const uint16_t dh = d == 0.0f ? (uint16_t) ((__builtin_bit_cast(uint32_t, mx) >> 16) & 0x8000u) ^ 0x8000u
+                                      : __builtin_bit_cast(uint16_t, (_Float16) d);
         o[0] = (uint8_t) (dh & 0xff); o[1] = (uint8_t) (dh >> 8);
         for (int j = 0; j < 16; j++) {
-            int q0 = (int8_t) (xb[j] * id + 8.5f), q1 = (int8_t) (xb[16 + j] * id + 8.5f);
+            const float x0 = xb[j] * id, x1 = xb[16 + j] * id;
+            int q0 = (int8_t) (x0 + 8.5f), q1 = (int8_t) (x1 + 8.5f);
             q0 = q0 > 15 ? 15 : q0;
             q1 = q1 > 15 ? 15 : q1;
             o[2 + j] = (uint8_t) (q0 | (q1 << 4));
@@ -431,14 +546,16 @@ static hipError_t launch_attn(const AttnArgs & a, uint32_t grid, hipStream_t st)
     return hipGetLastError();
 }
 
+// configurations (RT, WR, WK, NB). Decode: 8 waves split a 256-key tile (16 rows, 8 real). Mid: 64 rows. Verify /
+// prefill: 128 rows. Head dim 256 (the reference shape) keeps to at most 64 rows per workgroup (registers).
 template <int HD, int FMT>
 static hipError_t launch_attn_cfg(int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st) {
-    if constexpr (HD == 256) {   // head dim 256 (the reference shape): at most 64 rows per workgroup (registers)
-        if (cfg == CFG_DECODE) return launch_attn<HD, FMT, 1, 1, 2, 64>(a, grid, st);
+    if constexpr (HD == 256) {
+        if (cfg == CFG_DECODE) return launch_attn<HD, FMT, 1, 1, 4, 128>(a, grid, st);
         return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
     } else {
         switch (cfg) {
-            case CFG_DECODE: return launch_attn<HD, FMT, 1, 1, 2, 64>(a, grid, st);
+            case CFG_DECODE: return launch_attn<HD, FMT, 1, 1, 8, 256>(a, grid, st);
             case CFG_MID:    return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
             default:         return launch_attn<HD, FMT, 2, 4, 1, 64>(a, grid, st);   // verify / prefill
         }
@@ -459,10 +576,9 @@ hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32
 }
 
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
-    nb = 64;
-    if (cfg == CFG_DECODE) rows_per_wg = 16;
-    else if (cfg == CFG_MID || hd == 256) rows_per_wg = 64;
-    else rows_per_wg = 128;
+    if (cfg == CFG_DECODE) { rows_per_wg = 16; nb = hd == 128 ? 256 : 128; }
+    else if (cfg == CFG_MID || hd == 256) { rows_per_wg = 64; nb = 64; }
+    else { rows_per_wg = 128; nb = 64; }
 }
 
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
@@ -470,12 +586,6 @@ hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
     if (hd == 128) hipLaunchKernelGGL(merge_kernel<128>, dim3(grid), dim3(256), 0, st, a);
     else if (hd == 256) hipLaunchKernelGGL(merge_kernel<256>, dim3(grid), dim3(256), 0, st, a);
     else return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-
-hipError_t launch_qprep(const QprepArgs & a, hipStream_t st) {
-    const uint32_t n = a.nkv * a.qr * (a.hd / 32);
-    hipLaunchKernelGGL(qprep_kernel, dim3((n + 255) / 256), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -37,6 +37,7 @@ __global__ void normal_kernel(float * out, int64_t n, uint64_t seed, int64_t i0,
 // one thread per (key, head, 32-block)
 __global__ void fill_rows_kernel(uint8_t * rows, int fmt, int nkv, int hd, uint32_t rs, uint32_t hb, int64_t j0, int64_t n_keys,
                                  uint64_t seed, float amp, int n_out, const int32_t * ch, float mul) {
+    #pragma clang fp contract(off)   // round as written, like the oracle's generator
     const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     const int nblk = hd / 32;
     if (t >= n_keys * nkv * nblk) return;
@@ -65,10 +66,12 @@ __global__ void fill_rows_kernel(uint8_t * rows, int fmt, int nkv, int hd, uint3
         for (int e = 0; e < 32; e++) if (amax < fabsf(x[e])) { amax = fabsf(x[e]); mx = x[e]; }
         const float d = mx / -8.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        const uint16_t dh = __builtin_bit_cast(uint16_t, (_Float16) d);
+        const uint16_t dh = d == 0.0f ? (uint16_t) ((__builtin_bit_cast(uint32_t, mx) >> 16) & 0x8000u) ^ 0x8000u
+                                      : __builtin_bit_cast(uint16_t, (_Float16) d);
         o[0] = (uint8_t) (dh & 0xff); o[1] = (uint8_t) (dh >> 8);
         for (int e = 0; e < 16; e++) {
-            int q0 = (int8_t) (x[e] * id + 8.5f), q1 = (int8_t) (x[16 + e] * id + 8.5f);
+            const float x0 = x[e] * id, x1 = x[16 + e] * id;
+            int q0 = (int8_t) (x0 + 8.5f), q1 = (int8_t) (x1 + 8.5f);
             q0 = q0 > 15 ? 15 : q0;
             q1 = q1 > 15 ? 15 : q1;
             o[2 + e] = (uint8_t) (q0 | (q1 << 4));
