@@ -77,6 +77,8 @@ struct pa_hip_ws {
     float * po = nullptr; size_t po_cap = 0;
     unsigned int * ctr = nullptr; size_t ctr_cap = 0;
     float2 * pml = nullptr; size_t pml_cap = 0;
+    float * go = nullptr; size_t go_cap = 0;
+    float2 * gml = nullptr; size_t gml_cap = 0;
     unsigned long long * apart = nullptr; size_t apart_cap = 0;
     unsigned int * acount = nullptr;
     // the sme_* compatibility path: its own stream and staging buffers
@@ -105,7 +107,7 @@ extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
 extern "C" void pa_hip_ws_destroy(pa_hip_ws * w) {
     if (!w) return;
     (void) hipDeviceSynchronize();
-    hipFree(w->ctr); hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
+    hipFree(w->ctr); hipFree(w->go); hipFree(w->gml); hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
     hipFree(w->dk); hipFree(w->dv); hipFree(w->dq); hipFree(w->dout);
     if (w->stream) hipStreamDestroy(w->stream);
     delete w;
@@ -179,7 +181,7 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
 
     // split-K chunking per launch (pages go in groups of MAXP): about one workgroup per CU (PA_HIP_TARGET_WG), a chunk a
     // multiple of the key tile; a chunk may span pages
-    const int target = env_int("PA_HIP_TARGET_WG", 256);
+    const int target = env_int("PA_HIP_TARGET_WG", cfg == CFG_DECODE ? (decode_variant() == 2 ? 256 : decode_variant() == 1 ? 1024 : 512) : 256);
     const int forced_chunk = env_int("PA_HIP_CHUNK", 0);
     struct launch_t { int p0, np; uint32_t keys, chunk, n_chunks, slot0; };
     std::vector<launch_t> L;
@@ -200,15 +202,22 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         L.push_back({p0, np, keys, chunk, nch, n_slots});
         n_slots += nch;
     }
-    const bool fused = L.size() <= 1;   // one launch: its last workgroups fold the slots; else a separate merge kernel
+    // a separate merge kernel folds the slots (PA_HIP_SEPARATE_FOLD=0: the last workgroups of a single launch do)
+    const bool fused = L.size() <= 1 && env_int("PA_HIP_SEPARATE_FOLD", 1) == 0;
 
     // buffers: split-K slots and the fold counters
     const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
     const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
     if (!ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") || !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
         return -1;
-    if ((size_t) units * sizeof(unsigned int) > ws->ctr_cap) {
-        if (!ensure(ws->ctr, ws->ctr_cap, std::max<size_t>(units * sizeof(unsigned int), 4096), "hipMalloc counters") ||
+    const uint32_t n_groups = L.empty() ? 1 : (L[0].n_chunks + 7) / 8;   // first-level fold groups of 8 chunks
+    const size_t go_b = (size_t) n_groups * s->nkv * qr * s->hd * sizeof(float);
+    const size_t gml_b = (size_t) n_groups * s->nkv * qr * sizeof(float2);
+    if (!ensure(ws->go, ws->go_cap, go_b, "hipMalloc group slots") || !ensure(ws->gml, ws->gml_cap, gml_b, "hipMalloc group stats"))
+        return -1;
+    const size_t ctr_b = (size_t) units * (n_groups + 1) * sizeof(unsigned int);
+    if (ctr_b > ws->ctr_cap) {
+        if (!ensure(ws->ctr, ws->ctr_cap, std::max<size_t>(ctr_b, 4096), "hipMalloc counters") ||
             !hip_ok(hipMemset(ws->ctr, 0, ws->ctr_cap), "hipMemset counters"))   // once per growth; kernels keep them zero
             return -1;
     }
@@ -238,7 +247,7 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
         a.qmode = s->qmode; a.fused = fused ? 1u : 0u; a.scale = s->scale;
         a.s_mul = (s->qmode == PA_QMODE_GGML ? s->scale : 1.0f) * 1.4426950408889634f;
-        a.q = Q; a.po = ws->po; a.pml = ws->pml; a.counters = ws->ctr; a.O = O; a.m = m; a.l = l;
+        a.q = Q; a.po = ws->po; a.pml = ws->pml; a.counters = ws->ctr; a.go = ws->go; a.gml = ws->gml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
         if (!hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch")) return -1;
     }

@@ -8,6 +8,7 @@
 // key (orderable value << 32 | ~index) so that one unsigned max picks the largest value and, among equal values, the
 // lowest index. Each workgroup publishes its key; the last one to finish (device-scope counter, no waiting) folds the
 // row keys and computes (k, bonus). The counter is reset by that last workgroup, so no memset is needed between calls.
+// Only that workgroup acquires at device scope (an L2 invalidate); the others only release their key.
 #include "pa_attn.h"
 #include "pa_common.h"
 
@@ -52,13 +53,13 @@ __global__ __launch_bounds__(256) void accept_kernel(const AcceptArgs a) {
     if (t == 0) {
         best = umax64(umax64(red[0], red[1]), umax64(red[2], red[3]));
         __hip_atomic_store(&a.part[row * a.splits + sp], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();
-        const unsigned int done = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        // release at device scope (one L2 write-back); only the completing workgroup acquires (invalidates)
+        const unsigned int done = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         last = done == (unsigned int) (a.n_rows * a.splits - 1);
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // the last workgroup: fold each row's keys, then the accepted prefix
     __shared__ int32_t am[64];
     if (t < a.n_rows) {

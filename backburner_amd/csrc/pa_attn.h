@@ -26,7 +26,9 @@ struct AttnArgs {
     const float * q;                // [nkv][rows][hd] fp32
     float * po;                     // slots [slot][nkv][qr][hd]
     float2 * pml;                   // [slot][nkv][qr]: (max in base-2 units, sum)
-    unsigned int * counters;        // [nkv][nrb], zero between calls
+    unsigned int * counters;        // [nkv][nrb][n_groups + 1] fold counters, zero between calls
+    float * go;                     // first-level fold (group) slots [group][nkv][qr][hd]
+    float2 * gml;                   // [group][nkv][qr]
     float * O, * m, * l;            // final [nkv][rows][hd], [nkv][rows]
 };
 
@@ -41,6 +43,7 @@ hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb);
+int decode_variant();
 
 struct AcceptArgs {
     const float * logits;

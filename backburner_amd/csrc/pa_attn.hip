@@ -21,6 +21,8 @@
 #include "pa_attn.h"
 #include "pa_common.h"
 
+#include <cstdlib>
+
 namespace pa_hip {
 
 // ---------------------------------------------------------------- raw tile registers
@@ -175,6 +177,71 @@ struct TileIt {
     __device__ __forceinline__ bool valid(const AttnArgs & a, uint32_t key_hi) const { return p < a.n_pages && a.pstart[p] + jt < key_hi; }
 };
 
+// ---------------------------------------------------------------- split-K fold helpers
+constexpr uint32_t FOLD_G = 8;   // chunks per first-level fold group
+
+// count this workgroup's arrival at `ctr`; true for the workgroup that completes `expected` arrivals (it resets the
+// counter). Ordering: the barrier completes every wave's stores into the XCD's L2 (workgroup scope); thread 0's
+// increment is a release at device scope (one L2 write-back per workgroup, no invalidate); only the completing
+// workgroup acquires (invalidates), so the streaming workgroups keep their caches.
+template <int NT>
+__device__ __forceinline__ bool fold_arrive(unsigned int * ctr, uint32_t expected, int tid, bool & s_last) {
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned int done = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = done == expected - 1;
+        if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next call
+    }
+    __syncthreads();
+    if (!s_last) return false;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return true;
+}
+
+// fold n slots (slot i of head h, row r at ml[i*sstride + h*qr + r], o[(i*sstride + h*qr + r)*HD]) for rows [r0, r1):
+// online over batches of 8 slots (one round trip each). Writes the final (O, m in natural units, l) or group slot `gs`.
+template <int HD, int NT>
+__device__ __forceinline__ void fold_rows(const AttnArgs & a, uint32_t h, uint32_t r0, uint32_t r1, const float2 * ml, const float * o,
+                                          uint32_t n, size_t sstride, bool final, uint32_t gs, int tid) {
+    for (uint32_t e = tid; e < (r1 - r0) * (HD / 4); e += NT) {
+        const uint32_t row = r0 + e / (HD / 4), d4 = e % (HD / 4);
+        const size_t pr = (size_t) h * a.qr + row;
+        float M = -INFINITY, L = 0.0f;
+        pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t s0 = 0; s0 < n; s0 += 8) {
+            float2 mq[8];
+            pa_f4 oq[8];
+            #pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const bool in = s0 + q < n;
+                mq[q] = in ? ml[(s0 + q) * sstride + pr] : make_float2(-INFINITY, 0.0f);
+                oq[q] = in ? *(const pa_f4 *) (o + ((s0 + q) * sstride + pr) * HD + 4 * d4) : (pa_f4){0.f, 0.f, 0.f, 0.f};
+            }
+            float Mb = M;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) Mb = fmaxf(Mb, mq[q].x);
+            const float Ms = Mb == -INFINITY ? 0.0f : Mb;
+            const float sc = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Ms);
+            acc *= sc;
+            L *= sc;
+            #pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float wt = __builtin_amdgcn_exp2f(mq[q].x - Ms);   // an empty slot (-inf) weighs 0
+                L += wt * mq[q].y;
+                acc += wt * oq[q];
+            }
+            M = Mb;
+        }
+        if (final) {
+            *(pa_f4 *) (a.O + ((size_t) h * a.rows + row) * HD + 4 * d4) = acc;
+            if (d4 == 0) { a.m[(size_t) h * a.rows + row] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[(size_t) h * a.rows + row] = L; }
+        } else {
+            *(pa_f4 *) (a.go + (gs * sstride + pr) * HD + 4 * d4) = acc;
+            if (d4 == 0) a.gml[gs * sstride + pr] = make_float2(M, L);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- the attention kernel
 template <int HD, int FMT, int RT, int WR, int WK, int NB>
 __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
@@ -256,10 +323,10 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
         }
     }
     pa_f4 o[RT][ND];
-    float mrow[RT], lrow[RT];
+    float mref[RT], mtrue[RT], lrow[RT];
     #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        mrow[rt] = -INFINITY; lrow[rt] = 0.0f;
+        mref[rt] = mtrue[rt] = -INFINITY; lrow[rt] = 0.0f;
         #pragma unroll
         for (int d = 0; d < ND; d++) o[rt][d] = (pa_f4){0.f, 0.f, 0.f, 0.f};
     }
@@ -267,6 +334,7 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
 
     while (have) {
         const int nvalid = (int) min((uint32_t) NB, itr.j1 - itr.jt);
+        const bool full = nvalid == NB;
         __syncthreads();                                             // the previous tile's readers are done
         store_tile<HD, FMT, NB, NT>(R, Ks, Ksc, Vt, tid, s_mul);
         // next tile: its bytes fly while this one is computed
@@ -309,24 +377,35 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
             for (int rt = 0; rt < RT; rt++) {
                 float v[8];
                 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    v[i] = kbase + 4 * g + i < nvalid ? s[rt][0][i] : -INFINITY;
-                    v[4 + i] = kbase + 16 + 4 * g + i < nvalid ? s[rt][1][i] : -INFINITY;
+                for (int i = 0; i < 4; i++) { v[i] = s[rt][0][i]; v[4 + i] = s[rt][1][i]; }
+                if (!full) {
+                    #pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        if (kbase + 4 * g + i >= nvalid) v[i] = -INFINITY;
+                        if (kbase + 16 + 4 * g + i >= nvalid) v[4 + i] = -INFINITY;
+                    }
                 }
                 float tm = v[0];
                 #pragma unroll
                 for (int i = 1; i < 8; i++) tm = fmaxf(tm, v[i]);
                 tm = pa_wave_max16x4(tm);
-                const float mn = fmaxf(mrow[rt], tm);
-                const float ms = mn == -INFINITY ? 0.0f : mn;
-                const float alpha = __builtin_amdgcn_exp2f(mrow[rt] - ms);
+                mtrue[rt] = fmaxf(mtrue[rt], tm);
+                // the probabilities use a reference max that moves only when a score exceeds it by more than 2^8, so the
+                // O rescale runs rarely; p <= 256 stays well inside fp16. The exact max is kept in mtrue.
+                const bool need = tm > mref[rt] + 8.0f;
+                if (__any(need)) {
+                    const float nr = need ? mtrue[rt] : mref[rt];
+                    const float alpha = mref[rt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[rt] - nr);
+                    lrow[rt] *= alpha;
+                    #pragma unroll
+                    for (int d = 0; d < ND; d++) o[rt][d] *= alpha;
+                    mref[rt] = nr;
+                }
+                const float ms = mref[rt] == -INFINITY ? 0.0f : mref[rt];
                 float sum = 0.0f;
                 #pragma unroll
                 for (int i = 0; i < 8; i++) { v[i] = __builtin_amdgcn_exp2f(v[i] - ms); sum += v[i]; }
-                lrow[rt] = lrow[rt] * alpha + sum;
-                mrow[rt] = mn;
-                #pragma unroll
-                for (int d = 0; d < ND; d++) o[rt][d] *= alpha;
+                lrow[rt] += sum;
                 #pragma unroll
                 for (int i = 0; i < 8; i++) pf[rt][i] = (_Float16) v[i];
             }
@@ -342,9 +421,19 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
         }
     }
 
-    // ---- per-row sums over the 4 lane groups
+    // ---- per-row sums over the 4 lane groups; rebase (O, l) from the reference max to the exact max
+    float mrow[RT];
     #pragma unroll
-    for (int rt = 0; rt < RT; rt++) lrow[rt] = pa_wave_sum16x4(lrow[rt]);
+    for (int rt = 0; rt < RT; rt++) {
+        lrow[rt] = pa_wave_sum16x4(lrow[rt]);
+        const float f = mref[rt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[rt] - mtrue[rt]);
+        if (__any(f != 1.0f)) {
+            lrow[rt] *= f;
+            #pragma unroll
+            for (int d = 0; d < ND; d++) o[rt][d] *= f;
+        }
+        mrow[rt] = mtrue[rt];
+    }
 
     // ---- this workgroup's result: final (one chunk) or a split-K slot
     const bool direct = a.n_chunks == 1 && a.fused;
@@ -405,59 +494,21 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     }
     if (direct || !a.fused) return;
 
-    // ---- fused split-K fold: the last workgroup of this (head, row block) folds every slot
-    __threadfence();                                                  // publish this slot (device scope)
-    __syncthreads();
-    unsigned int * ctr = a.counters + h * a.nrb + rb;
-    if (tid == 0) {
-        const unsigned int done = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = done == a.n_chunks - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();                                                  // see every other slot
+    // ---- fused split-K fold, two levels: the last workgroup to finish in a group of FOLD_G consecutive chunks folds the
+    // group's slots into a group slot; the last group folder folds the group slots into the final (O, m, l). Counters
+    // are device-scope atomics (no waiting); each folder resets the counter it completed.
+    const uint32_t unit = h * a.nrb + rb;
+    const uint32_t n_groups = (a.n_chunks + FOLD_G - 1) / FOLD_G, grp = c / FOLD_G;
+    const uint32_t g0 = grp * FOLD_G, gn = min(a.n_chunks, g0 + FOLD_G) - g0;
     const size_t sstride = (size_t) a.nkv * a.qr;                    // rows between slots
-    const uint32_t r0 = rb * ROWS_WG, r1 = min(a.rows, r0 + ROWS_WG);
-    for (uint32_t e = tid; e < (r1 - r0) * (HD / 4); e += NT) {
-        const uint32_t row = r0 + e / (HD / 4), d4 = e % (HD / 4);
-        const float2 * ml = a.pml + (size_t) h * a.qr + row;
-        const float * op = a.po + ((size_t) h * a.qr + row) * HD + 4 * d4;
-        float M = -INFINITY;
-        uint32_t s = 0;
-        for (; s + 8 <= a.n_chunks; s += 8) {
-            float mm[8];
-            #pragma unroll
-            for (int q = 0; q < 8; q++) mm[q] = ml[(s + q) * sstride].x;
-            #pragma unroll
-            for (int q = 0; q < 8; q++) M = fmaxf(M, mm[q]);
-        }
-        for (; s < a.n_chunks; s++) M = fmaxf(M, ml[s * sstride].x);
-        const float Ms = M == -INFINITY ? 0.0f : M;
-        pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
-        float L = 0.0f;
-        s = 0;
-        for (; s + 8 <= a.n_chunks; s += 8) {
-            float2 mlq[8];
-            pa_f4 oq[8];
-            #pragma unroll
-            for (int q = 0; q < 8; q++) { mlq[q] = ml[(s + q) * sstride]; oq[q] = *(const pa_f4 *) (op + (s + q) * sstride * HD); }
-            #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const float wt = __builtin_amdgcn_exp2f(mlq[q].x - Ms);   // an empty slot (-inf) weighs 0
-                L += wt * mlq[q].y;
-                acc += wt * oq[q];
-            }
-        }
-        for (; s < a.n_chunks; s++) {
-            const float2 mq = ml[s * sstride];
-            const float wt = __builtin_amdgcn_exp2f(mq.x - Ms);
-            L += wt * mq.y;
-            acc += wt * *(const pa_f4 *) (op + s * sstride * HD);
-        }
-        *(pa_f4 *) (fO + (size_t) row * HD + 4 * d4) = acc;
-        if (d4 == 0) { fm[row] = M == -INFINITY ? -INFINITY : M * PA_LN2; fl[row] = L; }
-    }
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next call
+    if (!fold_arrive<NT>(a.counters + (size_t) unit * (n_groups + 1) + grp, gn, tid, s_last)) return;
+    // this workgroup folds group `grp` (its slots g0 .. g0+gn-1): into the final result if it is the only group
+    const bool final1 = n_groups == 1;
+    fold_rows<HD, NT>(a, h, rb * ROWS_WG, min(a.rows, (rb + 1) * ROWS_WG), a.pml + g0 * sstride, a.po + g0 * sstride * HD, gn, sstride,
+                      final1, grp, tid);
+    if (final1) return;
+    if (!fold_arrive<NT>(a.counters + (size_t) unit * (n_groups + 1) + n_groups, n_groups, tid, s_last)) return;
+    fold_rows<HD, NT>(a, h, rb * ROWS_WG, min(a.rows, (rb + 1) * ROWS_WG), a.gml, a.go, n_groups, sstride, true, 0, tid);
 }
 
 // ---------------------------------------------------------------- split-K fold as its own kernel
@@ -555,7 +606,12 @@ static hipError_t launch_attn_cfg(int cfg, const AttnArgs & a, uint32_t grid, hi
         return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
     } else {
         switch (cfg) {
-            case CFG_DECODE: return launch_attn<HD, FMT, 1, 1, 8, 256>(a, grid, st);
+            case CFG_DECODE:
+                switch (decode_variant()) {
+                    case 1: return launch_attn<HD, FMT, 1, 1, 2, 64>(a, grid, st);
+                    case 2: return launch_attn<HD, FMT, 1, 1, 8, 256>(a, grid, st);
+                    default: return launch_attn<HD, FMT, 1, 1, 4, 128>(a, grid, st);
+                }
             case CFG_MID:    return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
             default:         return launch_attn<HD, FMT, 2, 4, 1, 64>(a, grid, st);   // verify / prefill
         }
@@ -575,8 +631,17 @@ hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32
     return hipErrorInvalidValue;
 }
 
+int decode_variant() {
+    static const int v = getenv("PA_HIP_DECODE") ? atoi(getenv("PA_HIP_DECODE")) : 1;
+    return v;
+}
+
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
-    if (cfg == CFG_DECODE) { rows_per_wg = 16; nb = hd == 128 ? 256 : 128; }
+    if (cfg == CFG_DECODE) {
+        rows_per_wg = 16;
+        const int v = decode_variant();
+        nb = hd == 256 ? 128 : v == 1 ? 64 : v == 2 ? 256 : 128;
+    }
     else if (cfg == CFG_MID || hd == 256) { rows_per_wg = 64; nb = 64; }
     else { rows_per_wg = 128; nb = 64; }
 }
