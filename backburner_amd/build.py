@@ -27,8 +27,12 @@ HIP_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
 ]
 
+# per-source extras: the decode kernel keeps its MFMA accumulators in ordinary VGPRs (the compiler's AGPR choice would
+# copy them in and out of the matrix-core registers on every tile)
+SRC_FLAGS = {"pa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 LIBS = {
-    "libpa_hip.so": ["pa_attn.hip", "pa_accept.hip", "pa_abi.cpp"],
+    "libpa_hip.so": ["pa_attn.hip", "pa_decode.hip", "pa_accept.hip", "pa_abi.cpp"],
     "libpa_synth.so": ["pa_synth.hip"],
 }
 
@@ -51,7 +55,7 @@ def build(verbose: bool = False) -> None:
         for s in srcs:
             obj = BUILD / (s + ".o")
             lang = ["-x", "hip"] if s.endswith(".hip") else []
-            jobs.append([HIPCC, *HIP_FLAGS, *lang, "-c", str(CSRC / s), "-o", str(obj)])
+            jobs.append([HIPCC, *HIP_FLAGS, *SRC_FLAGS.get(s, []), *lang, "-c", str(CSRC / s), "-o", str(obj)])
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
     for lib, srcs in LIBS.items():

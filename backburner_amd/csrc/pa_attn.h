@@ -13,6 +13,7 @@ struct AttnArgs {
     const uint8_t * kp[MAXP];       // page base (key 0, head 0) of K / V
     const uint8_t * vp[MAXP];
     uint32_t pstart[MAXP + 1];      // key prefix: page p holds keys [pstart[p], pstart[p+1]) of the call
+    uint32_t cstart[MAXP + 1];      // decode kernel: chunk prefix, page p holds chunks [cstart[p], cstart[p+1])
     uint32_t n_pages, n_chunks, chunk, n_items;   // chunk = keys per workgroup; n_items = chunks x heads x row blocks
     uint32_t rs, hb, nkv;
     uint32_t rows;                  // real query rows per KV head
@@ -41,6 +42,7 @@ struct MergeArgs {
 
 hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st);
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st);
+hipError_t launch_decode(int fmt, int tpr, const AttnArgs & a, uint32_t grid, hipStream_t st);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb);
 int decode_variant();
