@@ -161,31 +161,24 @@ bool launch_fold(pa_hip_ws * ws, uint32_t n_slots, uint32_t nkv, uint32_t qr, ui
 // fold kernel
 int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
                 const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
-    const int tpr = env_int("PA_HIP_DEC_TPR", 2) == 1 ? 1 : 2;     // 32-key tiles per round (waves = 2 * tpr)
-    const uint32_t qr = 8, tile = 32u * (uint32_t) tpr;
-    const int target = std::max(1, env_int("PA_HIP_TARGET_WG", tpr == 2 ? 512 : 1024));
-    const int forced_chunk = env_int("PA_HIP_CHUNK", 0);
-    struct launch_t { int p0, np; uint32_t chunk, n_chunks, slot0; };
+    const uint32_t qr = 8, tile = 32;
+    // groups of tiles per head pair (group c takes the tiles c, c + G, ...): about PA_HIP_TARGET_WG workgroups in all
+    const int target = std::max(1, env_int("PA_HIP_TARGET_WG", 1024));
+    const int forced_groups = env_int("PA_HIP_GROUPS", 0);
+    struct launch_t { int p0, np; uint32_t n_groups, slot0; };
     std::vector<launch_t> L;
     uint32_t n_slots = 0;
     for (int p0 = 0; p0 < n_pages; p0 += MAXP) {
         const int np = std::min(MAXP, n_pages - p0);
-        uint64_t keys = 0;
-        for (int i = 0; i < np; i++) keys += nkeys[p0 + i];
-        if (keys == 0) continue;
-        uint64_t chunk;
-        if (forced_chunk > 0) chunk = (uint64_t) forced_chunk;
-        else {
-            const uint64_t want = std::max<uint64_t>(1, (uint64_t) target / (s->nkv / 2));   // chunks per head pair
-            chunk = (keys + want - 1) / want;
-        }
-        chunk = std::max<uint64_t>(tile, (chunk + tile - 1) / tile * tile);
-        uint32_t nch = 0;
-        for (int i = 0; i < np; i++) nch += (uint32_t) ((nkeys[p0 + i] + chunk - 1) / chunk);
-        L.push_back({p0, np, (uint32_t) chunk, nch, n_slots});
-        n_slots += nch;
+        uint64_t tiles = 0;
+        for (int i = 0; i < np; i++) tiles += (nkeys[p0 + i] + tile - 1) / tile;
+        if (tiles == 0) continue;
+        const uint64_t want = forced_groups > 0 ? (uint64_t) forced_groups : std::max<uint64_t>(1, (uint64_t) target / (s->nkv / 2));
+        const uint32_t ng = (uint32_t) std::min<uint64_t>(tiles, want);
+        L.push_back({p0, np, ng, n_slots});
+        n_slots += ng;
     }
-    const bool direct = L.size() == 1 && L[0].n_chunks == 1;
+    const bool direct = L.size() == 1 && L[0].n_groups == 1;
     if (!direct) {
         const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
         const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
@@ -198,25 +191,25 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
     for (const launch_t & ln : L) {
         AttnArgs a;
         std::memset(&a, 0, sizeof a);
-        uint32_t acc = 0, cacc = 0;
+        uint32_t acc = 0, tacc = 0;
         for (int i = 0; i < ln.np; i++) {
             a.kp[i] = (const uint8_t *) k_pages[ln.p0 + i];
             a.vp[i] = (const uint8_t *) v_pages[ln.p0 + i];
             a.pstart[i] = acc;
-            a.cstart[i] = cacc;
+            a.cstart[i] = tacc;                                      // tile prefix
             acc += nkeys[ln.p0 + i];
-            cacc += (nkeys[ln.p0 + i] + ln.chunk - 1) / ln.chunk;
+            tacc += (nkeys[ln.p0 + i] + tile - 1) / tile;
         }
         a.pstart[ln.np] = acc;
-        a.cstart[ln.np] = cacc;
-        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.chunk;
-        a.n_items = ln.n_chunks * (s->nkv / 2);
+        a.cstart[ln.np] = tacc;
+        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_groups; a.chunk = tile;
+        a.n_items = ln.n_groups * (s->nkv / 2);
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = 1; a.slot0 = ln.slot0;
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale;
         a.s_mul = s->scale * 1.4426950408889634f;
         a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
-        if (!hip_ok(launch_decode((int) s->fmt, tpr, a, grid, st), "decode launch")) return -1;
+        if (!hip_ok(launch_decode((int) s->fmt, a, grid, st), "decode launch")) return -1;
     }
     if (!direct && !launch_fold(ws, n_slots, s->nkv, qr, s->rows, (int) s->hd, O, m, l, st)) return -1;
     if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
@@ -248,7 +241,8 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
     }
     if (total > 0xffffffffull) { set_err("pa_hip_attn: more than 2^32 keys"); return -1; }
     hipStream_t st = (hipStream_t) stream;
-    // decode: <= 8 rows per KV head, quantized K/V with heads packed back to back, an even head count, 16-byte rows
+    // decode: <= 8 rows per KV head, quantized K/V with heads packed back to back, an even head count (the last head's
+    // 16-byte aligned slice then ends with the row), 16-byte rows
     if (s->qmode == PA_QMODE_GGML && (s->fmt == PA_FMT_Q8_0 || s->fmt == PA_FMT_Q4_0) && s->hd == 128 && s->rows <= 8 &&
         s->hb == head_bytes((int) s->fmt, 128) && s->nkv % 2 == 0 && s->rs % 16 == 0 && env_int("PA_HIP_DEC2", 1) != 0)
         return attn_decode(ws, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);

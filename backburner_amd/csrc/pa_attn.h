@@ -13,8 +13,9 @@ struct AttnArgs {
     const uint8_t * kp[MAXP];       // page base (key 0, head 0) of K / V
     const uint8_t * vp[MAXP];
     uint32_t pstart[MAXP + 1];      // key prefix: page p holds keys [pstart[p], pstart[p+1]) of the call
-    uint32_t cstart[MAXP + 1];      // decode kernel: chunk prefix, page p holds chunks [cstart[p], cstart[p+1])
+    uint32_t cstart[MAXP + 1];      // decode kernel: 32-key tile prefix, page p holds tiles [cstart[p], cstart[p+1])
     uint32_t n_pages, n_chunks, chunk, n_items;   // chunk = keys per workgroup; n_items = chunks x heads x row blocks
+                                                  // (decode kernel: n_chunks = tile groups, chunk = 32, items = groups x pairs)
     uint32_t rs, hb, nkv;
     uint32_t rows;                  // real query rows per KV head
     uint32_t qr;                    // padded rows per KV head in the slots
@@ -42,7 +43,7 @@ struct MergeArgs {
 
 hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st);
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st);
-hipError_t launch_decode(int fmt, int tpr, const AttnArgs & a, uint32_t grid, hipStream_t st);
+hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t st);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb);
 int decode_variant();

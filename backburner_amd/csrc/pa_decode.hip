@@ -1,12 +1,13 @@
 // pa_decode.hip - decode partial attention for up to 8 query rows per KV head (one token x GQA 8), q8_0 / q4_0 K and V,
 // ggml query rounding, head_dim 128 (gfx950).
 //
-// One workgroup = one pair of KV heads x one chunk of keys inside one page, 2*TPR waves: wave w computes head w % 2 of
-// tile w / 2 of every round (a round = TPR tiles of 32 keys). HBM traffic is fully coalesced: per round the workgroup
-// reads the pair's contiguous slice of every key row (2 x 136 bytes for q8_0) of K and V with 16-byte loads, lane by
-// lane along the rows (K by the first half of the waves, V by the second), two rounds ahead in registers. A round's
-// bytes are written raw into LDS; each wave then reads its head's K quants from there as the MFMA operand (unaligned
-// 16-byte LDS reads), and copies its V quants into its own block-aligned tile for the transposing reads.
+// One workgroup = one pair of KV heads x one group of 32-key tiles (every G-th tile of the call), two waves (one per
+// head) that share each tile. HBM traffic is coalesced: per tile wave 0 reads the pair's contiguous 16-byte aligned slice of every K
+// row (2 x 136 bytes for q8_0) and wave 1 the same of V, with 16-byte loads along the rows, two tiles ahead in
+// registers; both write their half raw into LDS. From there each lane takes its key's K quants as the MFMA operand and
+// copies the V quants into its wave's aligned tile, both read as whole aligned 16-byte chunks and byte-aligned in
+// registers (q8_0 blocks are 34 bytes, so their quants sit at 2-byte alignment; unaligned LDS reads run at a fraction
+// of the aligned rate). Rows are 16-byte multiples apart, so eight consecutive keys' chunks fall in distinct LDS banks.
 //
 // Per 32-key tile a wave computes:
 //   QK on the int8 matrix cores, exactly ggml's integer block dots. One v_mfma_i32_16x16x64_i8 per 32-dim quant block
@@ -52,8 +53,8 @@ constexpr float PMAX_LOG2 = 6.0f;         // p <= 2^6 between rescales (P' = p *
 
 template <int FMT> struct DecGeom {
     static constexpr int BB = FMT == 1 ? 34 : 18;          // bytes per quant block
-    static constexpr int HB = BB * DEC_NKB;                // bytes per head in a key row (136 / 72)
-    static constexpr int SL = 2 * HB;                      // a head pair's slice of a key row (272 / 144)
+    static constexpr int HB = BB * DEC_NKB;                // bytes per head in a key row (136 / 72, both 8 mod 16)
+    static constexpr int SL = 2 * HB;                      // a head pair's slice of a key row (272 / 144, 16-aligned)
     static constexpr int NCH = SL / 16;                    // 16-byte chunks per slice (17 / 9)
 };
 
@@ -82,155 +83,149 @@ __device__ __forceinline__ float dec_rowsum32(float v) {
 // LDS written by some lanes of a wave and read by others: DS instructions of one wave execute in order, so a
 // wavefront-scope fence (no instruction, only a compiler ordering point) is enough.
 __device__ __forceinline__ void dec_wave_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
-// workgroup barrier that orders LDS only: the vector-memory loads in flight (the next rounds) are not waited for
+
+// 16 bytes at byte offset S (compile-time) inside the 32 bytes of two consecutive aligned 16-byte LDS chunks x, y:
+// unaligned LDS reads run at a fraction of the aligned rate, so the rows are read as whole chunks and byte-aligned here
+template <int S> __device__ __forceinline__ pa_u4 dec_align(const pa_u4 & x, const pa_u4 & y) {
+    const uint32_t d[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+    constexpr int W = S / 4, B = S % 4;
+    pa_u4 r;
+    #pragma unroll
+    for (int j = 0; j < 4; j++) r[j] = B ? __builtin_amdgcn_alignbyte(d[W + j + 1], d[W + j], B) : d[W + j];
+    return r;
+}
+template <int S> __device__ __forceinline__ uint32_t dec_scale_bits(const pa_u4 & x) {   // the 16 bits at byte S - 2 of x
+    const uint32_t d[4] = {x.x, x.y, x.z, x.w};
+    constexpr int P = S - 2;
+    return (d[P / 4] >> (8 * (P % 4))) & 0xffffu;
+}
+
+// One quant block of one key from the wave's raw rows (16-byte aligned, the head's bytes at OFF): the 16 bytes the
+// lane needs (q8_0: half hh of the 32 quants; q4_0: all 16 nibble bytes) and the block's fp16 scale (bits), read as
+// whole aligned chunks. The scale sits in the 2 bytes before the quants: inside the first chunk read by the half-0 lane
+// unless the quants start a chunk (then a 16-bit read).
+template <int FMT, int OFF, int B>
+__device__ __forceinline__ void dec_block(const char * row, int hh, pa_u4 & q, uint32_t & sc) {
+    using G = DecGeom<FMT>;
+    constexpr int o = OFF + G::BB * B + 2, S = o & 15, C0 = o >> 4;
+    const char * c = row + 16 * C0 + (FMT == 1 ? 16 * hh : 0);
+    const pa_u4 x = *(const pa_u4 *) c;
+    if constexpr (S == 0) {
+        q = x;
+        sc = *(const uint16_t *) (row + o - 2);
+    } else {
+        const pa_u4 y = *(const pa_u4 *) (c + 16);
+        q = dec_align<S>(x, y);
+        sc = S >= 2 ? dec_scale_bits<(S >= 2 ? S : 2)>(x) : 0u;
+        if constexpr (FMT == 1) {                                    // the half-1 lane takes the half-0 lane's scale
+            const auto t = __builtin_amdgcn_permlane16_swap(sc, sc, false, false);
+            sc = t[0];
+        }
+    }
+}
+
+// the wave's tile from its raw rows: this lane's K operands and scales, V scales, and the V quants into the aligned tile
+// [key][32 * block] (q4_0: nibbles unpacked to bytes, element order)
+template <int FMT, int OFF>
+__device__ __forceinline__ void dec_unpack(const char * krow, const char * vrow, uint8_t * vdst, int hh, dec_v4i (&kq)[DEC_NKB],
+                                           float (&dkf)[DEC_NKB], pa_h2 (&dvh)[DEC_NKB]) {
+    #pragma unroll
+    for (int b = 0; b < DEC_NKB; b++) {
+        pa_u4 qk, qv;
+        uint32_t sk, sv;
+        switch (b) {
+            case 0: dec_block<FMT, OFF, 0>(krow, hh, qk, sk); dec_block<FMT, OFF, 0>(vrow, hh, qv, sv); break;
+            case 1: dec_block<FMT, OFF, 1>(krow, hh, qk, sk); dec_block<FMT, OFF, 1>(vrow, hh, qv, sv); break;
+            case 2: dec_block<FMT, OFF, 2>(krow, hh, qk, sk); dec_block<FMT, OFF, 2>(vrow, hh, qv, sv); break;
+            default: dec_block<FMT, OFF, 3>(krow, hh, qk, sk); dec_block<FMT, OFF, 3>(vrow, hh, qv, sv); break;
+        }
+        kq[b] = __builtin_bit_cast(dec_v4i, qk);
+        dkf[b] = pa_f16_bits_to_f32((uint16_t) sk);
+        const _Float16 dv = __builtin_bit_cast(_Float16, (uint16_t) sv);
+        dvh[b] = (pa_h2){dv, dv};
+        if constexpr (FMT == 2) {
+            const int sh = 4 * hh;
+            qv = (pa_u4){(qv.x >> sh) & 0x0f0f0f0fu, (qv.y >> sh) & 0x0f0f0f0fu, (qv.z >> sh) & 0x0f0f0f0fu, (qv.w >> sh) & 0x0f0f0f0fu};
+        }
+        *(pa_u4 *) (vdst + 32 * b + 16 * hh) = qv;
+    }
+}
+
+// LDS-only workgroup barrier: the vector-memory loads in flight (the next tiles) are not waited for
 __device__ __forceinline__ void dec_lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// 16 bytes at byte offset S (compile-time) past a 16-byte aligned LDS address, from naturally aligned dword reads and
-// byte alignment: unaligned LDS reads run at a fraction of the aligned rate
-template <int S> __device__ __forceinline__ pa_u4 dec_lds16(const char * base16) {
-    const uint32_t * p = (const uint32_t *) __builtin_assume_aligned(base16, 16);
-    constexpr int W = S / 4, B = S % 4;
-    uint32_t d[5];
-    #pragma unroll
-    for (int k = 0; k < (B ? 5 : 4); k++) d[k] = p[W + k];
-    pa_u4 r;
-    #pragma unroll
-    for (int j = 0; j < 4; j++) r[j] = B ? __builtin_amdgcn_alignbyte(d[j + 1], d[j], B) : d[j];
-    return r;
-}
-
-// this lane's K operands (16 quant bytes of each block; q8_0: half hh) and block scales from a raw key row (16-byte
-// aligned) of the round, for the head at slice offset HD * HB
-template <int FMT, int HD>
-__device__ __forceinline__ void dec_k_ops(const char * krow, int hh, dec_v4i (&kq)[DEC_NKB], float (&dkf)[DEC_NKB]) {
+template <int FMT>
+__global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     using G = DecGeom<FMT>;
-    #pragma unroll
-    for (int b = 0; b < DEC_NKB; b++) {
-        const int o = HD * G::HB + G::BB * b + 2;                    // quants of block b (compile-time after unrolling)
-        const char * base = krow + (o & ~15) + (FMT == 1 ? 16 * hh : 0);
-        switch (o & 15) {                                            // resolved at compile time
-            case 0: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<0>(base)); break;
-            case 2: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<2>(base)); break;
-            case 4: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<4>(base)); break;
-            case 6: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<6>(base)); break;
-            case 8: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<8>(base)); break;
-            case 10: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<10>(base)); break;
-            case 12: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<12>(base)); break;
-            default: kq[b] = __builtin_bit_cast(dec_v4i, dec_lds16<14>(base)); break;
-        }
-        dkf[b] = pa_f16_bits_to_f32(*(const uint16_t *) (krow + HD * G::HB + G::BB * b));
-    }
-}
-
-// V blocks of the wave's 32 keys from the raw round into the aligned tile [key][32 * block] (q4_0: nibbles unpacked to
-// bytes, element order), lane l: key l / 2, half l % 2. q8_0 block 3 is 8-byte aligned in the raw rows already and is
-// read from there.
-template <int FMT, int HD>
-__device__ __forceinline__ void dec_v_repack(const char * vtile, uint8_t * Vs, int lane) {
-    using G = DecGeom<FMT>;
-    const int key = lane >> 1, half = lane & 1;
-    const char * vrow = vtile + key * G::SL;
-    #pragma unroll
-    for (int b = 0; b < (FMT == 1 ? DEC_NKB - 1 : DEC_NKB); b++) {
-        const int o = HD * G::HB + G::BB * b + 2;
-        const char * base = vrow + (o & ~15) + (FMT == 1 ? 16 * half : 0);
-        pa_u4 x;
-        switch (o & 15) {
-            case 0: x = dec_lds16<0>(base); break;
-            case 2: x = dec_lds16<2>(base); break;
-            case 4: x = dec_lds16<4>(base); break;
-            case 6: x = dec_lds16<6>(base); break;
-            case 8: x = dec_lds16<8>(base); break;
-            case 10: x = dec_lds16<10>(base); break;
-            case 12: x = dec_lds16<12>(base); break;
-            default: x = dec_lds16<14>(base); break;
-        }
-        if constexpr (FMT == 2) {
-            const int sh = 4 * half;
-            x = (pa_u4){(x.x >> sh) & 0x0f0f0f0fu, (x.y >> sh) & 0x0f0f0f0fu, (x.z >> sh) & 0x0f0f0f0fu, (x.w >> sh) & 0x0f0f0f0fu};
-        }
-        *(pa_u4 *) (Vs + key * DEC_VST + 32 * b + 16 * half) = x;
-    }
-}
-
-template <int FMT, int TPR>
-__global__ __launch_bounds__(128 * TPR, 2) void dec_kernel(const AttnArgs a) {
-    using G = DecGeom<FMT>;
-    constexpr int NW = 2 * TPR;                                      // waves
-    constexpr int RK = 32 * TPR;                                     // keys per round
-    constexpr int TCH = RK * G::NCH;                                 // chunks per tensor per round
-    constexpr int LPT = 64 * NW / 2;                                 // lanes loading one tensor
-    constexpr int CPL = (TCH + LPT - 1) / LPT;                       // chunks per lane per round
-    constexpr int RAW = 2 * TCH * 16;                                // raw round bytes in LDS: K rows, then V rows
-    constexpr int COMB = NW * 8 * DEC_HD * 4 + NW * 8 * 16;         // end: per-wave O rows + (mref, mtrue, l)
-    constexpr int MAIN = RAW + NW * DEC_WLDS;
-    constexpr int LDS = MAIN > COMB ? MAIN : COMB;
+    constexpr int TCH = 32 * G::NCH;                                 // 16-byte chunks of one tensor's tile (544 / 288)
+    constexpr int CPL = (TCH + 63) / 64;                             // per lane of the wave that loads it (9 / 5)
+    constexpr int RAW = 2 * TCH * 16;                                // the tile's raw pair slices: K rows, then V rows
+    constexpr int LDS = RAW + 2 * DEC_WLDS;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
 
-    // ---- which (chunk, head pair): items chunk-major, pairs fastest; XCD x (= blockIdx % 8 in dispatch order) takes
-    // the contiguous item range [x*T8, (x+1)*T8), so the pairs of one chunk - neighbours in the same key rows - share an L2
+    // ---- which (group, head pair): the call's 32-key tiles are numbered across its pages (page p holds tiles
+    // [cstart[p], cstart[p+1])) and group c of NG takes tiles c, c + NG, c + 2 NG, ... - all workgroups stream through
+    // one narrow window of the cache instead of NG far-apart chunks, which the DRAM serves faster. Items group-major, pairs
+    // fastest; XCD x (= blockIdx % 8 in dispatch order) takes the contiguous item range [x*T8, (x+1)*T8), so the pairs of
+    // one tile - neighbours in the same key rows - share an L2.
     const uint32_t bid = blockIdx.x, xcd = bid % 8, local = bid / 8;
     const uint32_t t8 = (a.n_items + 7) / 8;
     const uint32_t w = xcd * t8 + local;
     if (local >= t8 || w >= a.n_items) return;
     const uint32_t npair = a.nkv / 2;
     const uint32_t pr = w % npair, c = w / npair;
-    uint32_t p = 0;
-    while (a.cstart[p + 1] <= c) p++;                                // the page holding chunk c
-    const uint32_t k0 = (c - a.cstart[p]) * a.chunk;
-    const uint32_t k1 = min(k0 + a.chunk, a.pstart[p + 1] - a.pstart[p]);
+    const uint32_t NG = a.n_chunks, T = a.cstart[a.n_pages];
     const uint32_t rs = a.rs;
 
     const int tid = threadIdx.x, lane = tid % 64;
-    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);      // uniform: the round loop is a scalar loop
-    const int hd = wave & 1, ts = wave >> 1;                         // this wave's head in the pair, tile in the round
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);      // uniform: the tile loop is a scalar loop
+    const int hd = wave;                                             // this wave's head in the pair; it loads K (0) or V (1)
     const uint32_t h = 2 * pr + hd;
     const int g = lane >> 4, n = lane & 15, hh = g & 1;
     const int kap = 16 * (g >> 1) + n;                               // this lane's key in the tile
 
-    char * raw = smem;                                               // [2][RK keys][SL]: the round's K, V slices
+    char * raw = smem;                                               // [2][32 keys][SL]
     char * wl = smem + RAW + wave * DEC_WLDS;
     uint8_t * Vs = (uint8_t *) wl;                                   // [32 keys][DEC_VST] int8 V, block-aligned
     char * Pl = wl + 32 * DEC_VST;                                   // [NKB][32 keys][8 rows] fp16 P'
     char * Qt = Pl + DEC_NKB * DEC_PBLK;                             // [NKB][DEC_QBLK] int8 query operands
     float * Ct = (float *) (Qt + DEC_NKB * DEC_QBLK);                // [NKB][8] scales, then [NKB][8] q4_0 starts
 
-    // ---- load roles: the first NW/2 waves load K, the rest V; chunk q = i*LPT + lt of the tensor's round is key q / NCH,
-    // bytes 16 * (q % NCH) of the pair slice
-    const bool ldv = wave >= NW / 2;
-    const int lt = tid - (ldv ? 64 * NW / 2 : 0);
-    const uint8_t * tbase = (ldv ? a.vp[p] : a.kp[p]) + (size_t) pr * G::SL;
+    // ---- tile loads: wave 0 loads K, wave 1 V; chunk q = 64 i + lane is key q / NCH, bytes 16 * (q % NCH) of the pair
+    // slice; rows past the page's end reload its last row (masked later)
     uint32_t qkey[CPL], qoff[CPL];
     #pragma unroll
     for (int i = 0; i < CPL; i++) {
-        const int q = min(i * LPT + lt, TCH - 1);                    // a lane past the round's chunks reloads the last
+        const int q = min(64 * i + lane, TCH - 1);                   // a lane past the tile's chunks reloads the last
         qkey[i] = (uint32_t) (q / G::NCH);
         qoff[i] = 16u * (uint32_t) (q % G::NCH);
     }
-    auto round_load = [&](pa_u4 (&X)[CPL], uint32_t jr) {
-        const uint32_t last = k1 - 1 - jr;                           // the round's last valid key (rows past it reload it)
+    auto page_of = [&](uint32_t tau, uint32_t & pg) { while (a.cstart[pg + 1] <= tau) pg++; };   // pages only advance
+    auto tile_load = [&](pa_u4 (&X)[CPL], uint32_t pg, uint32_t j0, uint32_t last) {   // rows j0 + min(key, last)
+        const uint8_t * tb = (hd ? a.vp[pg] : a.kp[pg]) + (size_t) pr * G::SL;
         #pragma unroll
         for (int i = 0; i < CPL; i++) {
-            const uint32_t row = jr + min(qkey[i], last);
-            X[i] = pa_ld<pa_u4>(tbase + (size_t) row * rs + qoff[i]);
+            const uint32_t row = j0 + min(qkey[i], last);
+            X[i] = pa_ld<pa_u4>(tb + (size_t) row * rs + qoff[i]);
         }
     };
-    auto round_store = [&](const pa_u4 (&X)[CPL]) {
-        char * dst = raw + (ldv ? TCH * 16 : 0) + 16 * lt;
+    auto tile_store = [&](const pa_u4 (&X)[CPL]) {
+        char * dst = raw + hd * TCH * 16 + 16 * lane;
         #pragma unroll
         for (int i = 0; i < CPL; i++)
-            if (i < CPL - 1 || (CPL - 1) * LPT + lt < TCH) *(pa_u4 *) (dst + 16 * i * LPT) = X[i];
+            if (i < CPL - 1 || 64 * (CPL - 1) + lane < TCH) *(pa_u4 *) (dst + 16 * 64 * i) = X[i];
     };
 
-    // ---- the query rows' loads first, then the first two rounds' loads, so that the query preparation waits only for
+    // ---- the query rows' loads first, then the first two tiles' loads, so that the query preparation waits only for
     // its own loads (memory counters are in order). Lane (g, n): row n % 8 (row 0 when past the rows, then zeroed),
     // elements 16*(g%2) .. +15 of every block.
     const int qr8 = n & 7;
     const bool qlive = qr8 < (int) a.rows;
+    const uint32_t qmask = qlive ? 0xffffffffu : 0u;
     pa_f4 qx[DEC_NKB][4];
     {
         const float * qrow = a.q + ((size_t) h * a.rows + (qlive ? qr8 : 0)) * DEC_HD + 16 * hh;
@@ -240,11 +235,21 @@ __global__ __launch_bounds__(128 * TPR, 2) void dec_kernel(const AttnArgs a) {
             for (int j = 0; j < 4; j++) qx[b][j] = *(const pa_f4 *) (qrow + 32 * b + 4 * j);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t nround = (k1 - k0 + RK - 1) / RK;                 // >= 1: the chunk is not empty
-    pa_u4 X0[CPL], X1[CPL];                                          // rounds 0, 2, 4, ... and 1, 3, 5, ...
-    round_load(X0, k0);
+    const uint32_t ntiles = (T - c + NG - 1) / NG;                   // >= 1: c < NG <= T
+    uint32_t pl = 0, pc = 0;                                         // pages of the next tile to load / to compute
+    auto load_tile = [&](pa_u4 (&X)[CPL], uint32_t tau) {            // tile tau, or a cheap dummy (one row) past the end
+        if (tau < T) {
+            page_of(tau, pl);
+            const uint32_t j0 = 32 * (tau - a.cstart[pl]);
+            tile_load(X, pl, j0, a.pstart[pl + 1] - a.pstart[pl] - 1 - j0);
+        } else {
+            tile_load(X, pl, 0, 0);
+        }
+    };
+    pa_u4 X0[CPL], X1[CPL];                                          // tiles c, c + 2 NG, ... and c + NG, c + 3 NG, ...
+    load_tile(X0, c);
     __builtin_amdgcn_sched_barrier(0);                               // X0's loads strictly before X1's (in-order counts)
-    round_load(X1, nround > 1 ? k0 + RK : k0);
+    load_tile(X1, c + NG);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- query rows: ggml's q8_0 of each 32-block (d = amax/127, id = 1/d, q = roundf(x*id), d -> fp16;
@@ -258,8 +263,10 @@ __global__ __launch_bounds__(128 * TPR, 2) void dec_kernel(const AttnArgs a) {
         for (int b = 0; b < DEC_NKB; b++) {
             float x[16];
             #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const pa_f4 v = qlive ? qx[b][j] : (pa_f4){0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 4; j++) {                            // a dead row is zeroed by a mask, so that the loads
+                // stay where they were issued (whole vectors are bit-cast: clang's bit_cast of one ext-vector element
+                // reads element 0)
+                const pa_f4 v = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, qx[b][j]) & qmask);
                 x[4 * j] = v[0]; x[4 * j + 1] = v[1]; x[4 * j + 2] = v[2]; x[4 * j + 3] = v[3];
             }
             float am = 0.0f;
@@ -302,39 +309,27 @@ __global__ __launch_bounds__(128 * TPR, 2) void dec_kernel(const AttnArgs a) {
     const _Float16 cb = FMT == 1 ? (_Float16) (-128.0f / 16777216.0f) : (_Float16) (-136.0f / 16777216.0f);
     const pa_h8 cneg = {cb, cb, cb, cb, cb, cb, cb, cb};
     float * arow = (float *) Pl;                                     // rescale factors by row (rare path scratch)
+    const char * krow = raw + kap * G::SL, * vrow = raw + TCH * 16 + kap * G::SL;
+    uint8_t * vdst = Vs + kap * DEC_VST;
 
-    // this wave's tile in the raw round: this lane's K and V key rows (pair slices, 16-byte aligned), the V rows
-    const char * krow = raw + (32 * ts + kap) * G::SL;
-    const char * vrow = krow + TCH * 16;
-    const char * vtile = raw + TCH * 16 + 32 * ts * G::SL;
-
-    uint32_t jr = k0;
-    auto round = [&](pa_u4 (&X)[CPL]) {
-        dec_lds_barrier();                                           // every wave is done reading the previous round
-        round_store(X);
-        {   // this register set's next round (two rounds ahead; past the chunk's end it reloads the last rows)
-            const uint32_t jn = jr + 2 * RK < k1 ? jr + 2 * RK : jr;
-            round_load(X, jn);
-        }
-        dec_lds_barrier();                                           // the round's raw bytes are visible
-        const uint32_t jt = jr + 32 * ts;
-        const int nvalid = jt < k1 ? (int) min(32u, k1 - jt) : 0;
-        if (nvalid == 0) return;                                     // uniform: this wave's tile is past the chunk
+    auto tile = [&](pa_u4 (&X)[CPL], uint32_t tau) {
+        // ---- the tile's raw pair slices -> LDS (this wave's tensor), then this register set's next tile (two steps
+        // ahead; past the last one a dummy load that nothing reads)
+        page_of(tau, pc);
+        const int nvalid = (int) min(32u, a.pstart[pc + 1] - a.pstart[pc] - 32 * (tau - a.cstart[pc]));
+        dec_lds_barrier();                                           // both waves are done reading the previous tile
+        tile_store(X);
+        load_tile(X, tau + 2 * NG);
+        dec_lds_barrier();                                           // the tile's raw bytes are visible
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- from the raw round: this lane's K operands and scales, V scales; the V quants -> the wave's aligned tile.
-        // Byte offsets of the head inside the pair slice differ by 8 (mod 16), so each head has its own (compile-time)
-        // alignment; the branch is uniform.
+        // ---- this lane's key: K operands and scales, V scales; V quants -> the aligned tile. The head's offset in the
+        // pair slice (0 or HB) fixes every alignment at compile time; the branch is uniform.
         dec_v4i kq[DEC_NKB];
         float dkf[DEC_NKB];
         pa_h2 dvh[DEC_NKB];
-        if (hd == 0) { dec_k_ops<FMT, 0>(krow, hh, kq, dkf); dec_v_repack<FMT, 0>(vtile, Vs, lane); }
-        else { dec_k_ops<FMT, 1>(krow, hh, kq, dkf); dec_v_repack<FMT, 1>(vtile, Vs, lane); }
-        #pragma unroll
-        for (int b = 0; b < DEC_NKB; b++) {
-            const _Float16 dv = __builtin_bit_cast(_Float16, *(const uint16_t *) (vrow + hd * G::HB + G::BB * b));
-            dvh[b] = (pa_h2){dv, dv};
-        }
+        if (hd) dec_unpack<FMT, G::HB>(krow, vrow, vdst, hh, kq, dkf, dvh);
+        else dec_unpack<FMT, 0>(krow, vrow, vdst, hh, kq, dkf, dvh);
         dec_wave_sync();
         __builtin_amdgcn_sched_barrier(0);
 
@@ -342,15 +337,15 @@ __global__ __launch_bounds__(128 * TPR, 2) void dec_kernel(const AttnArgs a) {
         dec_v4i T[DEC_NKB];
         #pragma unroll
         for (int b = 0; b < DEC_NKB; b++) {
-            dec_v4i kb = kq[b];
+            dec_v4i kb4 = kq[b];
             if constexpr (FMT == 2) {
                 const int sh = 4 * hh;
-                kb = (dec_v4i){(int) (((uint32_t) kb.x >> sh) & 0x0f0f0f0fu), (int) (((uint32_t) kb.y >> sh) & 0x0f0f0f0fu),
-                               (int) (((uint32_t) kb.z >> sh) & 0x0f0f0f0fu), (int) (((uint32_t) kb.w >> sh) & 0x0f0f0f0fu)};
+                kb4 = (dec_v4i){(int) (((uint32_t) kb4.x >> sh) & 0x0f0f0f0fu), (int) (((uint32_t) kb4.y >> sh) & 0x0f0f0f0fu),
+                                (int) (((uint32_t) kb4.z >> sh) & 0x0f0f0f0fu), (int) (((uint32_t) kb4.w >> sh) & 0x0f0f0f0fu)};
             }
             const dec_v4i qa = *(const dec_v4i *) (Qt + b * DEC_QBLK + qoffa);
             const dec_v4i qc = FMT == 2 ? *(const dec_v4i *) (Ct + DEC_NKB * 8 + b * 8 + 4 * hh) : (dec_v4i){0, 0, 0, 0};
-            T[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa, kb, qc, 0, 0, 0);
+            T[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa, kb4, qc, 0, 0, 0);
         }
 
         // ---- base-2 scores relative to the reference max: S = -mref + sum_b (dot_b * dq_b * s_mul) * dk_b
@@ -413,10 +408,8 @@ __global__ __launch_bounds__(128 * TPR, 2) void dec_kernel(const AttnArgs a) {
             const pa_h8 pb = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
             #pragma unroll
             for (int db = 2 * b; db < 2 * b + 2; db++) {
-                const char * vsrc = (FMT == 1 && b == DEC_NKB - 1)
-                    ? vtile + (8 * g + (n >> 1)) * G::SL + hd * G::HB + G::BB * b + 2 + 16 * (db & 1) + 8 * (n & 1)
-                    : (const char *) Vs + (8 * g + (n >> 1)) * DEC_VST + 16 * db + 8 * (n & 1);
-                const dec_v2i rv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((DEC_LDS dec_v2i *) vsrc);
+                const dec_v2i rv = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                    (DEC_LDS dec_v2i *) (Vs + (8 * g + (n >> 1)) * DEC_VST + 16 * db + 8 * (n & 1)));
                 const uint32_t x0 = (uint32_t) rv.x ^ 0x80808080u, x1 = (uint32_t) rv.y ^ 0x80808080u;
                 const pa_u4 u = {pa_perm(x0, x0, 0x0c010c00u), pa_perm(x0, x0, 0x0c030c02u), pa_perm(x1, x1, 0x0c010c00u),
                                  pa_perm(x1, x1, 0x0c030c02u)};
@@ -428,74 +421,51 @@ __global__ __launch_bounds__(128 * TPR, 2) void dec_kernel(const AttnArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         dec_wave_sync();
     };
-    // pairs of rounds, then an odd last one: no exit between the two halves, so the load order (X0's batch before X1's)
-    // is the same on every path into a round and the wait before each round covers only its own batch
-    for (uint32_t r = 0; r + 1 < nround; r += 2) {
-        round(X0);
-        jr += RK;
-        round(X1);
-        jr += RK;
+    // pairs of tiles, then an odd last one: no exit between the two halves, so the load order (X0's batch before X1's)
+    // is the same on every path into a tile and the wait before each tile covers only its own batch
+    uint32_t tau = c;
+    for (uint32_t t = 0; t + 1 < ntiles; t += 2) {
+        tile(X0, tau);
+        tile(X1, tau + NG);
+        tau += 2 * NG;
     }
-    if (nround & 1) round(X0);
+    if (ntiles & 1) tile(X0, tau);
 
-    // ---- wave state -> LDS: O rows (lanes n < 8), (mref, exact max, sum) per row
-    float lt4[4], mt[4];
+    // ---- this wave's head: rows' (sum, exact max) over the lanes; O rebased from the reference max to the exact one
+    // and written from lanes n < 8 (final result for a single group, else the group's split-K slot)
+    float lt4[4], mt4[4], f4[4];
     #pragma unroll
     for (int i = 0; i < 4; i++) {
         lt4[i] = dec_rowsum32(lsum[i]);
-        mt[i] = dec_rowmax32(mxr[i]) - nm[i];                      // -inf for a wave without keys
-    }
-    __syncthreads();                                                 // every wave is done with its tiles
-    float * cO = (float *) smem;                                     // [NW][8][HD]
-    float * cS = cO + NW * 8 * DEC_HD;                               // [NW][8][4]: mref, mtrue, l
-    if (n < 8) {
-        #pragma unroll
-        for (int d = 0; d < DEC_ND; d++) *(pa_f4 *) (cO + ((size_t) wave * 8 + n) * DEC_HD + 16 * d + 4 * g) = O[d];
-    }
-    if (n == 0 && g < 2) {
-        #pragma unroll
-        for (int i = 0; i < 4; i++) *(pa_f4 *) (cS + (wave * 8 + 4 * g + i) * 4) = (pa_f4){mref[i], mt[i], lt4[i], 0.0f};
-    }
-    __syncthreads();
-
-    // ---- merge the waves of each head (waves hd, hd + 2, ...); write the final result (one chunk) or a split-K slot
-    const bool direct = a.n_chunks == 1 && a.fused;
-    const uint32_t nrows = min(a.rows, 8u);
-    for (uint32_t e = tid; e < 2 * nrows * (DEC_HD / 4); e += 64 * NW) {
-        const uint32_t eh = e / (nrows * (DEC_HD / 4)), er = e % (nrows * (DEC_HD / 4));
-        const uint32_t r = er / (DEC_HD / 4), d4 = er % (DEC_HD / 4);
-        const uint32_t hw = 2 * pr + eh;
-        float M = -INFINITY;
-        #pragma unroll
-        for (int t = 0; t < TPR; t++) M = fmaxf(M, cS[((2 * t + eh) * 8 + r) * 4 + 1]);
-        pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
-        float L = 0.0f;
-        if (M != -INFINITY) {
-            #pragma unroll
-            for (int t = 0; t < TPR; t++) {
-                const int q = 2 * t + eh;
-                const pa_f4 st = *(const pa_f4 *) (cS + (q * 8 + r) * 4);
-                const float wt = st[0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st[0] - M);
-                L += wt * st[2];
-                acc += (wt * 16777216.0f) * *(const pa_f4 *) (cO + ((size_t) q * 8 + r) * DEC_HD + 4 * d4);
-            }
+        mt4[i] = dec_rowmax32(mxr[i]) - nm[i];                     // the exact max (base 2); -inf without keys
+        f4[i] = mref[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[i] - mt4[i]);
+        if (n == 0 && g < 2) {                                       // row 4*hh + i: the factor for the O lanes
+            arow[4 * g + i] = f4[i] * 16777216.0f;                   // (the accumulator holds O * 2^-24)
+            arow[8 + 4 * g + i] = mt4[i];
+            arow[16 + 4 * g + i] = lt4[i] * f4[i];
         }
-        if (direct) {
-            *(pa_f4 *) (a.O + ((size_t) hw * a.rows + r) * DEC_HD + 4 * d4) = acc;
-            if (d4 == 0) { a.m[(size_t) hw * a.rows + r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[(size_t) hw * a.rows + r] = L; }
-        } else {
-            const size_t slot = a.slot0 + c;
-            *(pa_f4 *) (a.po + ((slot * a.nkv + hw) * a.qr + r) * DEC_HD + 4 * d4) = acc;
-            if (d4 == 0) a.pml[(slot * a.nkv + hw) * a.qr + r] = make_float2(M, L);
+    }
+    dec_wave_sync();
+    const bool direct = a.n_chunks == 1 && a.fused;
+    const uint32_t r = n & 7;
+    if (n < 8 && r < a.rows) {
+        const float fo = arow[r], M = arow[8 + r], L = arow[16 + r];
+        #pragma unroll
+        for (int d = 0; d < DEC_ND; d++) {
+            const pa_f4 v = O[d] * fo;
+            if (direct) *(pa_f4 *) (a.O + ((size_t) h * a.rows + r) * DEC_HD + 16 * d + 4 * g) = v;
+            else *(pa_f4 *) (a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r) * DEC_HD + 16 * d + 4 * g) = v;
+        }
+        if (g == 0) {
+            if (direct) { a.m[(size_t) h * a.rows + r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[(size_t) h * a.rows + r] = L; }
+            else a.pml[((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r] = make_float2(M, L);
         }
     }
 }
 
-hipError_t launch_decode(int fmt, int tpr, const AttnArgs & a, uint32_t grid, hipStream_t st) {
-    if (fmt == 1 && tpr == 1) hipLaunchKernelGGL((dec_kernel<1, 1>), dim3(grid), dim3(128), 0, st, a);
-    else if (fmt == 1 && tpr == 2) hipLaunchKernelGGL((dec_kernel<1, 2>), dim3(grid), dim3(256), 0, st, a);
-    else if (fmt == 2 && tpr == 1) hipLaunchKernelGGL((dec_kernel<2, 1>), dim3(grid), dim3(128), 0, st, a);
-    else if (fmt == 2 && tpr == 2) hipLaunchKernelGGL((dec_kernel<2, 2>), dim3(grid), dim3(256), 0, st, a);
+hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t st) {
+    if (fmt == 1) hipLaunchKernelGGL((dec_kernel<1>), dim3(grid), dim3(128), 0, st, a);
+    else if (fmt == 2) hipLaunchKernelGGL((dec_kernel<2>), dim3(grid), dim3(128), 0, st, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
