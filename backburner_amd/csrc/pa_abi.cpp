@@ -187,8 +187,8 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
     }
     const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
     ws->ev0 = ws->ev1 = nullptr;
-    if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
-    for (const launch_t & ln : L) {
+    for (size_t li = 0; li < L.size(); li++) {
+        const launch_t & ln = L[li];
         AttnArgs a;
         std::memset(&a, 0, sizeof a);
         uint32_t acc = 0, tacc = 0;
@@ -209,10 +209,16 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
         a.s_mul = s->scale * 1.4426950408889634f;
         a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
-        if (!hip_ok(launch_decode((int) s->fmt, a, grid, st), "decode launch")) return -1;
+        // the timing events (if any) at the start of the first and the end of the last decode kernel
+        if (!hip_ok(launch_decode((int) s->fmt, a, grid, st, li == 0 ? ev0 : nullptr, li + 1 == L.size() ? ev1 : nullptr),
+                    "decode launch"))
+            return -1;
+    }
+    if (L.empty()) {   // no keys: the events bracket nothing
+        if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
+        if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
     }
     if (!direct && !launch_fold(ws, n_slots, s->nkv, qr, s->rows, (int) s->hd, O, m, l, st)) return -1;
-    if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
     return 0;
 }
 
@@ -325,13 +331,13 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
         if (!hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch")) return -1;
     }
+    if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;   // the attention kernel alone
     if (!fused) {
         MergeArgs ma;
         ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
         ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
         if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
     }
-    if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
     return 0;
 }
 

@@ -33,6 +33,7 @@
 // arithmetic for the scores (restated in oracle/pa_oracle.c, orc_attn_ggml).
 #include "pa_attn.h"
 #include "pa_common.h"
+#include <hip/hip_ext.h>
 
 namespace pa_hip {
 
@@ -463,9 +464,10 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     }
 }
 
-hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t st) {
-    if (fmt == 1) hipLaunchKernelGGL((dec_kernel<1>), dim3(grid), dim3(128), 0, st, a);
-    else if (fmt == 2) hipLaunchKernelGGL((dec_kernel<2>), dim3(grid), dim3(128), 0, st, a);
+hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    // the events (optional) are recorded by the launch itself at the kernel's start and end
+    if (fmt == 1) hipExtLaunchKernelGGL((dec_kernel<1>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a);
+    else if (fmt == 2) hipExtLaunchKernelGGL((dec_kernel<2>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

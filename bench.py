@@ -2,16 +2,18 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary] [--no-cpu]
 
-Headline workload (BASELINE configs[1]): decode at long context, 64 layers in sequence, each layer = 1 query token x 64
+Headline workload: decode at long context, 64 layers in sequence, each layer = 1 query token x 64
 query heads over 8 KV heads (GQA 8), head dim 128, 131,072 old q8_0 positions in 32 pages of 4,096 keys, K with 4 x8
 outlier channels per head, 64 distinct seeded caches (18.25 GB in HBM, made on the device by libpa_synth). A step is
-one pass over the 64 layers: per layer one pa_hip_attn call (Q prep + split-K attention + merge) on one stream.
+one pass over the 64 layers: per layer one pa_hip_attn call (split-K attention kernel + merge kernel) on one stream.
 
-Printed: ONE JSON line. value = microseconds per layer (lower is better); roofline = the attention kernel's
-algorithmic bytes per launch / its mean duration (HIP events recorded by the library around that kernel, on its
-stream); cpu_baseline = the oracle's ggml-faithful restatement (oracle/pa_oracle.c, OpenMP over rows) timed on this
-host's cores over a bounded sample of layer 0's keys and scaled to a full layer. --secondary adds the other BASELINE
-configs (4k decode, 16-token verify, 512-token prefill, q4_0 decode/verify, fused acceptance) as "secondary" entries.
+Printed: ONE JSON line. value = microseconds per layer of the whole call sequence (lower is better); roofline = the
+decode kernel's algorithmic bytes per launch / its mean duration (start/end events recorded by the kernel launch itself,
+on its stream), traffic = HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
+cpu_baseline = the oracle's ggml-faithful restatement (oracle/pa_oracle.c, OpenMP over rows) timed on this host's cores
+over the first --cpu-layers layers at full size, with the GPU's layer-0 output checked against it (parity_vs_cpu).
+--secondary adds the other workloads (4k decode, 16-token verify, 512-token prefill, q4_0 decode/verify, fused
+acceptance) as "secondary" entries.
 """
 from __future__ import annotations
 
@@ -46,6 +48,7 @@ class Layers:
         self.rs = nkv * self.hb
         syn = bb.synth()
         self.bufs = []
+        self.kv = []
         self.pages = []
         self.q = []
         import oracle as orc   # only for the outlier channel picks (a few ints), shared with the oracle generator
@@ -63,6 +66,7 @@ class Layers:
                                        [vb.ptr + i * PAGE * self.rs for i in range(np_)],
                                        [min(PAGE, n_keys - i * PAGE) for i in range(np_)], []))
             self.bufs += [kb, vb, qb] + ([ch] if ch else [])
+            self.kv.append((kb, vb))
             self.q.append(qb)
         bb.device_sync()
         r = nkv * rows
@@ -141,35 +145,39 @@ def measured_copy_bw(bb, nbytes=2 << 30):
     return res
 
 
-def cpu_baseline(bb, lay: Layers, sample_keys: int):
-    """Time the oracle's ggml-faithful CPU restatement on layer 0's first sample_keys keys, all rows, all host cores;
-    also check the GPU on exactly that sample against it."""
+def cpu_baseline(bb, lay: Layers, n_layers: int):
+    """Time the oracle's ggml-faithful CPU restatement over the first n_layers layers of the workload at full size (all
+    keys, all rows, every host core), and check the GPU's layer-0 output against the CPU's on the same bytes."""
     import oracle as orc
-    rs = lay.rs
-    kb = lay.bufs[0].download(np.uint8, sample_keys * rs)
-    vb = lay.bufs[1].download(np.uint8, sample_keys * rs)
-    q = lay.q[0].download(np.float32).reshape(-1, lay.hd)
     s = orc.make_shape(lay.nkv, lay.rows, lay.hd, lay.fmt)
     threads = len(os.sched_getaffinity(0))
-    t0 = time.perf_counter()
-    O, m, l = orc.attn_ggml(s, q, kb, vb, sample_keys, threads)
-    dt = time.perf_counter() - t0
-    # the GPU on the same sample (pages of the first sample_keys keys)
-    np_ = (sample_keys + PAGE - 1) // PAGE
-    pages = bb.Pages(lay.pages[0].k[:np_], lay.pages[0].v[:np_], [min(PAGE, sample_keys - i * PAGE) for i in range(np_)], [])
-    ws = bb.Workspace()
-    ws.attn(lay.shape, pages, lay.q[0].ptr, lay.O, lay.m, lay.l)
-    bb.device_sync()
     r = lay.nkv * lay.rows
-    ml = lay.out.download(np.float32, 2 * r, offset=r * lay.hd * 4)
-    Og = lay.out.download(np.float32, r * lay.hd).reshape(r, lay.hd)
-    eo, em, el = orc.rel_err(Og, ml[:r], ml[r:], O, m, l)
+    nbytes = lay.n_keys * lay.rs
+    total = 0.0
+    parity = None
+    ws = bb.Workspace()
+    for L in range(n_layers):
+        kb = lay.kv[L][0].download(np.uint8, nbytes)
+        vb = lay.kv[L][1].download(np.uint8, nbytes)
+        q = lay.q[L].download(np.float32).reshape(-1, lay.hd)
+        t0 = time.perf_counter()
+        O, m, l = orc.attn_ggml(s, q, kb, vb, lay.n_keys, threads)
+        total += time.perf_counter() - t0
+        if L == 0:
+            ws.attn(lay.shape, lay.pages[0], lay.q[0].ptr, lay.O, lay.m, lay.l)
+            bb.device_sync()
+            ml = lay.out.download(np.float32, 2 * r, offset=r * lay.hd * 4)
+            Og = lay.out.download(np.float32, r * lay.hd).reshape(r, lay.hd)
+            eo, em, el = orc.rel_err(Og, ml[:r], ml[r:], O, m, l)
+            parity = {"max_rel_O": eo, "max_rel_m": em, "max_rel_l": el, "layer": 0, "keys": lay.n_keys, "tol": 2e-3}
+        del kb, vb
     ws.close()
-    per_layer_us = dt * 1e6 * lay.n_keys / sample_keys
+    per_layer_us = total * 1e6 / n_layers
     return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"layer 0, keys [0, {sample_keys}) of {lay.n_keys}, all {r} rows, oracle/pa_oracle.c orc_attn_ggml "
-                      f"(ggml-faithful, q8_0 int block dots, OpenMP {threads} threads) {dt:.2f} s, scaled x{lay.n_keys / sample_keys:g}",
-            }, {"max_rel_O": eo, "max_rel_m": em, "max_rel_l": el, "keys": sample_keys, "tol": 2e-3}
+            "sample": f"layers 0..{n_layers - 1} of {lay.n_layers} at full size ({lay.n_keys} keys, all {r} rows), "
+                      f"oracle/pa_oracle.c orc_attn_ggml (ggml-faithful: q8_0 int block dots, online softmax, fp32 V "
+                      f"accumulation; OpenMP over rows, {threads} threads), {total:.2f} s of CPU time in all",
+            }, parity
 
 
 def read_traffic(name: str):
@@ -204,17 +212,16 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=64)
-    ap.add_argument("--secondary", action="store_true", help="also run the other BASELINE configs")
+    ap.add_argument("--secondary", action="store_true", help="also run the other workloads (4k decode, verify, prefill, q4_0, acceptance)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-keys", type=int, default=16384)
+    ap.add_argument("--cpu-layers", type=int, default=64, help="layers of the workload the CPU baseline runs")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU position sharding is a design note only (DESIGN.md)",
+        print(json.dumps({"error": "one GPU only: sharding the old pages by position range over several GPUs is a design note, not built",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
     import backburner_amd as bb
-    name = (bytes(64))
     import ctypes as C
     nb = C.create_string_buffer(64)
     n_cu = bb.synth().pa_synth_device_name(nb, 64)
@@ -226,7 +233,7 @@ def main():
     lay, head, total_ms, kern = run_config(bb, ws, bb.FMT_Q8_0, args.layers, 131072, 8, args.steps, args.warmup,
                                            "decode 1 token x 64 q-heads / 8 kv-heads, hd 128, 131072 q8_0 keys, 64 layers")
     log("headline", json.dumps(head))
-    cpu, parity = (None, None) if args.no_cpu else cpu_baseline(bb, lay, args.cpu_keys)
+    cpu, parity = (None, None) if args.no_cpu else cpu_baseline(bb, lay, max(1, min(args.cpu_layers, args.layers)))
     lay.close()
 
     secondary = []
@@ -257,7 +264,7 @@ def main():
                    "layers": args.layers, "global_batch": 1, "seq_len": 131072, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode128k"),
-                     "kernel": "attn_kernel<128, q8_0, decode>", "alg_bytes_per_launch": alg,
+                     "kernel": "pa_hip::dec_kernel<1> (q8_0 decode)", "alg_bytes_per_launch": alg,
                      "kernel_us_mean": round(kmean_s * 1e6, 3)},
         "hbm_frac_call": round(alg / (head["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "measured_bw_gbs": {k: round(v, 1) for k, v in bw.items()},

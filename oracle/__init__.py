@@ -1,6 +1,6 @@
 """Python view of the CPU oracle (liboracle.so, pa_oracle.c). TEST INFRASTRUCTURE ONLY: imported by tests/, by
-__graft_entry__.smoke() and by bench.py's cpu_baseline leg, as the checker or the timed CPU baseline - never by the
-product package.
+__graft_entry__.smoke() and by bench.py's cpu_baseline leg, as the reference for parity checks or the timed CPU
+baseline - never by the product package.
 """
 from __future__ import annotations
 

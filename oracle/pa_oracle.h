@@ -1,8 +1,8 @@
 /* pa_oracle.h - CPU oracle for the phone-attn old-KV partial-attention path.
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product library links or calls this; only tests/, the smoke check in
- * __graft_entry__.py and bench.py's cpu_baseline leg load liboracle.so, and only as the checker (or as the timed CPU
- * baseline), never as the thing measured or shipped.
+ * __graft_entry__.py and bench.py's cpu_baseline leg load liboracle.so, and only as the parity reference (or as the
+ * timed CPU baseline), never as the thing measured or shipped.
  *
  * What it restates (reference paths relative to the StayLameBro/backburner checkout):
  *   - row / block formats: q8_0 34-byte blocks (fp16 d + 32 int8), q4_0 18-byte blocks (fp16 d + 16 bytes, byte i = element

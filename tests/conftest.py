@@ -10,7 +10,7 @@ if str(ROOT) not in sys.path:
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device; runs on the GPU box")
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device")
 
 
 @pytest.fixture(scope="session")

@@ -1,6 +1,6 @@
 """GPU parity of the device engine path (pa_hip_attn, through the C ABI) against the CPU oracle on the same bytes.
 
-Tolerance (written here): 2e-3 relative on O (per row, after rebasing to the oracle's max), on m
+Tolerance: 2e-3 relative on O (per row, after rebasing to the oracle's max), on m
 (relative to max(1, |m|)) and on l, against the ggml-faithful restatement (orc_attn_ggml) in PA_QMODE_GGML, and against
 the fp64 closed form with the reference engines' rounding (f16(q*scale)) in PA_QMODE_F16."""
 import os
