@@ -222,6 +222,77 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
     return 0;
 }
 
+// many rows per KV head (verify, prefill; head dim 128): mma_kernel over row blocks of 32*NW rows x chunks of tiles
+int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+             const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
+    const uint32_t tile = 32;
+    const int nw_env = env_int("PA_HIP_MMA_NW", 0);
+    const uint32_t nw = nw_env == 2 || nw_env == 4 || nw_env == 8 ? (uint32_t) nw_env : s->rows > 128 ? 8u : s->rows > 64 ? 4u : 2u;
+    const uint32_t nrb = (s->rows + 32 * nw - 1) / (32 * nw), qr = nrb * 32 * nw;
+    const uint32_t units = s->nkv * nrb;
+    // key chunks: about PA_HIP_MMA_TARGET workgroups in all (resident ones: 1 of 8 waves, 2 of 4, 4 of 2 per CU)
+    const int target = std::max(1, env_int("PA_HIP_MMA_TARGET", nw == 8 ? 512 : 1024));
+    struct launch_t { int p0, np; uint32_t tpc, n_chunks, slot0; };
+    std::vector<launch_t> L;
+    uint32_t n_slots = 0;
+    for (int p0 = 0; p0 < n_pages; p0 += MAXP) {
+        const int np = std::min(MAXP, n_pages - p0);
+        uint64_t tiles = 0;
+        for (int i = 0; i < np; i++) tiles += (nkeys[p0 + i] + tile - 1) / tile;
+        if (tiles == 0) continue;
+        const uint64_t want = std::max<uint64_t>(1, (uint64_t) target / units);
+        const uint64_t tpc = (tiles + want - 1) / want;
+        const uint32_t nch = (uint32_t) ((tiles + tpc - 1) / tpc);
+        L.push_back({p0, np, (uint32_t) tpc, nch, n_slots});
+        n_slots += nch;
+    }
+    const bool direct = L.size() == 1 && L[0].n_chunks == 1;
+    if (!direct) {
+        const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
+        const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
+        if (!ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") || !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
+            return -1;
+    }
+    const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
+    ws->ev0 = ws->ev1 = nullptr;
+    for (size_t li = 0; li < L.size(); li++) {
+        const launch_t & ln = L[li];
+        AttnArgs a;
+        std::memset(&a, 0, sizeof a);
+        uint32_t acc = 0, tacc = 0;
+        for (int i = 0; i < ln.np; i++) {
+            a.kp[i] = (const uint8_t *) k_pages[ln.p0 + i];
+            a.vp[i] = (const uint8_t *) v_pages[ln.p0 + i];
+            a.pstart[i] = acc;
+            a.cstart[i] = tacc;
+            acc += nkeys[ln.p0 + i];
+            tacc += (nkeys[ln.p0 + i] + tile - 1) / tile;
+        }
+        a.pstart[ln.np] = acc;
+        a.cstart[ln.np] = tacc;
+        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.tpc;
+        a.n_items = ln.n_chunks * units;
+        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
+        a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale; a.s_mul = 1.4426950408889634f;
+        a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
+        const uint32_t grid = (a.n_items + 7) / 8 * 8;
+        if (!hip_ok(launch_mma((int) s->fmt, (int) nw, a, grid, st, li == 0 ? ev0 : nullptr, li + 1 == L.size() ? ev1 : nullptr),
+                    "mma launch"))
+            return -1;
+    }
+    if (L.empty()) {
+        if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
+        if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
+    }
+    if (!direct) {
+        MergeArgs ma;
+        ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
+        ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
+    }
+    return 0;
+}
+
 }  // namespace
 
 extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
@@ -252,6 +323,9 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
     if (s->qmode == PA_QMODE_GGML && (s->fmt == PA_FMT_Q8_0 || s->fmt == PA_FMT_Q4_0) && s->hd == 128 && s->rows <= 8 &&
         s->hb == head_bytes((int) s->fmt, 128) && s->nkv % 2 == 0 && s->rs % 16 == 0 && env_int("PA_HIP_DEC2", 1) != 0)
         return attn_decode(ws, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
+    // more rows (verify, prefill), head dim 128, heads packed at hb >= the head size, 16-byte aligned Q rows
+    if (s->hd == 128 && env_int("PA_HIP_MMA", 1) != 0)
+        return attn_mma(ws, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
 
     const int cfg = pick_cfg(s->rows, s->hd);
     int rows_wg = 16, nb = 64;

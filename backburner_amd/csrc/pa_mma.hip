@@ -1,0 +1,348 @@
+// pa_mma.hip - partial attention for many query rows per KV head (16-token verify, 512-token prefill chunks, and any
+// shape with more than 8 rows) over q8_0 / q4_0 / f16 K and V, head dim 128, fp16 matrix cores (gfx950).
+//
+// One workgroup = one KV head x one block of 32*NW query rows x one chunk of consecutive 32-key tiles; NW waves, 32
+// rows each. Per tile the workgroup dequantizes K and V once into LDS as fp16 (d*q rounded once: the quants become
+// fp16 integers exactly through the 0x64 exponent byte, then one subtract and one multiply), double-buffered, with the
+// next tile's raw bytes already in flight into registers. Each wave then computes, with v_mfma_f32_32x32x16_f16,
+//   S^T (32 keys x 32 rows) = K . Q'^T      (8 MFMAs over the 128 dims; Q' stays in registers for the whole kernel),
+// so lane (h, n) holds row n's scores of keys 8j + 4h + i (j, i < 4) - which is exactly the B operand layout of
+//   O^T (128 dims x 32 rows) += V^T . P^T    (4 dim blocks x 2 MFMAs; V^T read from LDS by ds_read_b64_tr_b16),
+// so the probabilities never leave registers, and every value a lane holds belongs to its own row n: the running max
+// and sum need one exchange with lane n + 32 per tile and no LDS.
+//
+// Q' is the query as fp16: PA_QMODE_GGML converts Q to K's vec_dot type as ggml's CPU flash_attn_ext does - q8_0 per
+// 32-block for quantized K (quantize_row_q8_0_ref), taken as fp16(d*q*scale), and fp16(q) for f16 K (the scale then
+// multiplies the score); PA_QMODE_F16 takes fp16(q*scale) (the reference engines' Qs, phone-attn.h:595-599). Online softmax in base 2 with a
+// reference max that moves only when a score exceeds it by more than 2^MM_PMAX (O is rescaled rarely); the exact max
+// is tracked beside it and applied at the end. Output: one split-K slot per workgroup (O unnormalised against the
+// base-2 max, max, sum), folded by merge_kernel, or the final (O, m, l) when the call has a single chunk.
+//
+// Reference roles: pa_attn_big + pa_big_load (pa-metal.mm:379-487: per (row tile, KV head, key chunk) dequantize a
+// K/V block into threadgroup memory as half, S = QK^T on the matrix units, online softmax with key masking, O = a O +
+// PV, write a slot); ggml's q8_0 query conversion (restated in oracle/pa_oracle.c, orc_attn_ggml).
+#include "pa_attn.h"
+#include "pa_common.h"
+#include <hip/hip_ext.h>
+
+namespace pa_hip {
+
+typedef _Float16 mm_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mm_h2 __attribute__((ext_vector_type(2)));
+typedef float mm_f16 __attribute__((ext_vector_type(16)));
+typedef __fp16 mm_tr4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+#define MM_LDS __attribute__((address_space(3)))
+
+constexpr int MM_HD = 128;
+constexpr int MM_KST = 2 * MM_HD + 16;            // K tile row stride (bytes): 16 consecutive keys' 16-byte reads hit
+                                                  // distinct banks
+constexpr int MM_VST = 2 * MM_HD + 64;            // V tile row stride: the 4 rows x 64 bytes of a half-wave's
+                                                  // transposing reads hit distinct banks
+constexpr int MM_KT = 32 * MM_KST, MM_VT = 32 * MM_VST, MM_STAGE = MM_KT + MM_VT;
+constexpr float MM_PMAX = 6.0f;                   // p <= 2^6 between rescales
+constexpr float MM_LOG2E = 1.4426950408889634f;
+
+template <int FMT> struct MmFmt {
+    static constexpr int BB = FMT == 1 ? 34 : FMT == 2 ? 18 : 64;    // bytes per 32-value block
+};
+
+// raw bytes of one staging unit = (tensor, key, block, half): 16 values of one 32-block and the block scale
+template <int FMT> struct MmRaw {
+    pa_u4 q[FMT == 0 ? 2 : 1];
+    uint32_t d;
+};
+
+template <int FMT>
+__device__ __forceinline__ void mm_load_unit(MmRaw<FMT> & r, const uint8_t * blk, int half) {
+    if constexpr (FMT == 1) {
+        r.q[0] = pa_ld<pa_u4>(blk + 2 + 16 * half);
+        r.d = pa_ld<uint16_t>(blk);
+    } else if constexpr (FMT == 2) {
+        r.q[0] = pa_ld<pa_u4>(blk + 2);
+        r.d = pa_ld<uint16_t>(blk);
+    } else {
+        r.q[0] = pa_ld<pa_u4>(blk + 32 * half);
+        r.q[1] = pa_ld<pa_u4>(blk + 32 * half + 16);
+        r.d = 0;
+    }
+}
+
+// 16 values -> fp16 (8 dwords). Quantized formats: byte u (unsigned quant) -> fp16 bits 0x6400 | u = 1024 + u exactly,
+// minus (1024 + bias) exactly, times d (one rounding).
+template <int FMT>
+__device__ __forceinline__ void mm_dequant(const MmRaw<FMT> & r, int half, pa_u4 & lo, pa_u4 & hi) {
+    if constexpr (FMT == 0) {
+        lo = r.q[0]; hi = r.q[1];
+    } else {
+        pa_u4 u = r.q[0];
+        if constexpr (FMT == 1) {
+            u = u ^ 0x80808080u;                                          // int8 -> uint8 (q + 128)
+        } else {
+            const int sh = 4 * half;                                      // q4_0: low nibbles = values 0-15
+            u = (u >> sh) & 0x0f0f0f0fu;
+        }
+        constexpr float bias = FMT == 1 ? 1152.0f : 1032.0f;              // 1024 + 128 / 1024 + 8
+        const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t) r.d);
+        const mm_h2 d2 = {dh, dh}, b2 = {(_Float16) bias, (_Float16) bias};
+        uint32_t w[8];
+        #pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t x = u[c];
+            const mm_h2 a = __builtin_bit_cast(mm_h2, pa_perm(0x64646464u, x, 0x04010400u));   // bytes 0, 1
+            const mm_h2 b = __builtin_bit_cast(mm_h2, pa_perm(0x64646464u, x, 0x04030402u));   // bytes 2, 3
+            w[2 * c] = __builtin_bit_cast(uint32_t, (mm_h2) ((a - b2) * d2));
+            w[2 * c + 1] = __builtin_bit_cast(uint32_t, (mm_h2) ((b - b2) * d2));
+        }
+        lo = (pa_u4){w[0], w[1], w[2], w[3]};
+        hi = (pa_u4){w[4], w[5], w[6], w[7]};
+    }
+}
+
+__device__ __forceinline__ void mm_lds_barrier() {   // LDS-only workgroup barrier: loads in flight are not waited for
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// v_permlane32_swap of a value with itself gives every lane the pair (value of lane l % 32, value of lane l % 32 + 32)
+__device__ __forceinline__ float mm_max32(float v) {    // max over lanes l and l ^ 32
+    const auto t = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned) t[0]), __builtin_bit_cast(float, (unsigned) t[1]));
+}
+__device__ __forceinline__ float mm_sum32(float v) {    // sum over lanes l and l ^ 32
+    const auto t = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+    return __builtin_bit_cast(float, (unsigned) t[0]) + __builtin_bit_cast(float, (unsigned) t[1]);
+}
+
+template <int FMT, int NW>
+__global__ __launch_bounds__(64 * NW) void mma_kernel(const AttnArgs a) {
+    constexpr int NT = 64 * NW;
+    constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
+    static_assert(UPT * NT == 512, "NW must be 2, 4 or 8");
+    __shared__ __attribute__((aligned(16))) char smem[2 * MM_STAGE];
+
+    // ---- which (chunk, KV head, row block): row blocks fastest, so the workgroups that share a chunk's K/V run side
+    // by side on one XCD (= blockIdx % 8 in dispatch order, which takes a contiguous item range) and share its L2
+    const uint32_t bid = blockIdx.x, xcd = bid % 8, local = bid / 8;
+    const uint32_t t8 = (a.n_items + 7) / 8;
+    const uint32_t w = xcd * t8 + local;
+    if (local >= t8 || w >= a.n_items) return;
+    const uint32_t rb = w % a.nrb, h = (w / a.nrb) % a.nkv, c = w / (a.nrb * a.nkv);
+    const uint32_t T = a.cstart[a.n_pages];                          // 32-key tiles of the call
+    const uint32_t t0 = c * a.chunk, t1 = min(t0 + a.chunk, T);      // this chunk's tiles [t0, t1)
+    const uint32_t ntiles = t1 - t0;                                  // >= 1
+
+    const int tid = threadIdx.x, lane = tid % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int n = lane & 31, h2 = lane >> 5;
+    const uint32_t row = rb * (32 * NW) + 32 * wave + n;             // this lane's query row (within the KV head)
+    const bool rlive = row < a.rows;
+
+    // ---- staging units of this thread: u = tid + NT*i -> tensor u >> 8, key (u >> 3) & 31, block (u >> 1) & 3,
+    // half u & 1; rows past the page's end reload its last row (masked later)
+    using F = MmFmt<FMT>;
+    MmRaw<FMT> R[UPT];
+    uint32_t pl = 0, pc = 0;                                         // pages of the next tile to load / to compute
+    auto page_of = [&](uint32_t tau, uint32_t & pg) { while (a.cstart[pg + 1] <= tau) pg++; };
+    auto load_tile = [&](uint32_t tau) {
+        page_of(tau, pl);
+        const uint32_t j0 = 32 * (tau - a.cstart[pl]);
+        const uint32_t last = a.pstart[pl + 1] - a.pstart[pl] - 1 - j0;
+        #pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + NT * i;
+            const int tensor = u >> 8, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
+            const uint8_t * base = (tensor ? a.vp[pl] : a.kp[pl]) + (size_t) h * a.hb;
+            const uint32_t r = j0 + min((uint32_t) key, last);
+            mm_load_unit<FMT>(R[i], base + (size_t) r * a.rs + blk * F::BB, half);
+        }
+    };
+    auto store_tile = [&](int stage) {
+        char * st = smem + stage * MM_STAGE;
+        #pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + NT * i;
+            const int tensor = u >> 8, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
+            pa_u4 lo, hi;
+            mm_dequant<FMT>(R[i], half, lo, hi);
+            char * dst = tensor ? st + MM_KT + key * MM_VST : st + key * MM_KST;
+            dst += 2 * (32 * blk + 16 * half);
+            *(pa_u4 *) dst = lo;
+            *(pa_u4 *) (dst + 16) = hi;
+        }
+    };
+
+    // ---- the first tile's loads, then the query rows (B operand: lane (h2, n) holds row n, dims 16kk + 8h2 + t)
+    load_tile(t0);
+    __builtin_amdgcn_sched_barrier(0);
+    mm_h8 Qf[8];
+    {
+        const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * MM_HD + 8 * h2;
+        const uint32_t qmask = rlive ? 0xffffffffu : 0u;
+        pa_f4 x[16];
+        #pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            x[2 * kk] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 16 * kk)) & qmask);
+            x[2 * kk + 1] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 16 * kk + 4)) & qmask);
+        }
+        const float scale = a.scale;
+        if (a.qmode == 0 && FMT != 0) {                              // PA_QMODE_GGML, quantized K: Q -> q8_0
+            // ggml q8_0 per 32-block b = k-steps 2b, 2b+1: this lane holds 16 of its values, lane ^ 32 the other 16
+            #pragma clang fp contract(off)
+            #pragma unroll
+            for (int b = 0; b < 4; b++) {
+                float am = 0.0f;
+                #pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const pa_f4 v = x[4 * b + j];
+                    am = fmaxf(am, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+                }
+                am = mm_max32(am);
+                const float d = am / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                const float dq = (float) (_Float16) d * scale;        // the fp16 block scale (as ggml stores it) * scale
+                #pragma unroll
+                for (int kq = 0; kq < 2; kq++) {
+                    mm_h8 f;
+                    #pragma unroll
+                    for (int t = 0; t < 8; t++) {
+                        const float xv = x[4 * b + 2 * kq + t / 4][t % 4];
+                        f[t] = (_Float16) (roundf(xv * id) * dq);
+                    }
+                    Qf[2 * b + kq] = f;
+                }
+            }
+        } else {                                                     // f16(q * scale), or f16(q) for f16 K in
+            const float qs = a.qmode == 0 ? 1.0f : scale;             // PA_QMODE_GGML (ggml's f16 vec_dot type)
+            #pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                mm_h8 f;
+                #pragma unroll
+                for (int t = 0; t < 8; t++) f[t] = (_Float16) (x[2 * kk + t / 4][t % 4] * qs);
+                Qf[kk] = f;
+            }
+        }
+    }
+
+    // ---- prologue: tile t0 -> stage 0, tile t0 + 1's loads in flight
+    store_tile(0);
+    if (ntiles > 1) load_tile(t0 + 1);
+    mm_lds_barrier();
+
+    mm_f16 O[4];
+    #pragma unroll
+    for (int db = 0; db < 4; db++) O[db] = (mm_f16){};
+    float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
+    const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit
+
+    for (uint32_t t = 0; t < ntiles; t++) {
+        const int stage = t & 1;
+        // the next tile's bytes -> the other stage (last read before the previous barrier), then the one after's loads
+        if (t + 1 < ntiles) {
+            store_tile(stage ^ 1);
+            if (t + 2 < ntiles) load_tile(t0 + t + 2);
+        }
+        const uint32_t tau = t0 + t;
+        page_of(tau, pc);
+        const int nvalid = (int) min(32u, a.pstart[pc + 1] - a.pstart[pc] - 32 * (tau - a.cstart[pc]));
+        const char * Kt = smem + stage * MM_STAGE;
+        const char * Vt = Kt + MM_KT;
+
+        // ---- S^T = K Q'^T
+        mm_f16 S = (mm_f16){};
+        #pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            const mm_h8 kf = *(const mm_h8 *) (Kt + n * MM_KST + 32 * kk + 16 * h2);
+            S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, Qf[kk], S, 0, 0, 0);
+        }
+        if (nvalid < 32) {                                           // keys 8j + 4h2 + i past the page's end
+            #pragma unroll
+            for (int v = 0; v < 16; v++)
+                if (8 * (v / 4) + 4 * h2 + (v % 4) >= nvalid) S[v] = -INFINITY;
+        }
+        float tm = S[0];
+        #pragma unroll
+        for (int v = 1; v < 16; v++) tm = fmaxf(tm, S[v]);
+        tm = mm_max32(tm) * sm;                   // row n's tile max, base 2
+        if (__builtin_amdgcn_ballot_w64(tm > mref + MM_PMAX)) {
+            // rare: move the reference max of every row that needs it (uniform branch)
+            const float mn = fmaxf(mref, tm);
+            const float alpha = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mn);
+            #pragma unroll
+            for (int db = 0; db < 4; db++) O[db] *= alpha;
+            lsum *= alpha;
+            mref = mn;
+        }
+        mx = fmaxf(mx, tm);
+        float p[16];
+        #pragma unroll
+        for (int v = 0; v < 16; v++) {
+            p[v] = __builtin_amdgcn_exp2f(fmaf(S[v], sm, -mref));
+            lsum += p[v];
+        }
+        mm_h8 P[2];
+        #pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+            #pragma unroll
+            for (int t8 = 0; t8 < 8; t8++) P[mi][t8] = (_Float16) p[8 * mi + t8];
+
+        // ---- O^T += V^T P^T: per dim block and 16-key half, V^T by two transposing reads (lane 16q + s reads key
+        // row 16mi + (8 for the second read) + 4(q >> 1) + s / 4, dims 32db + 16(q & 1) + 4(s % 4) .. +3)
+        const int q4 = lane >> 4, s4 = lane & 15;
+        #pragma unroll
+        for (int db = 0; db < 4; db++) {
+            #pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                const char * vb = Vt + (16 * mi + 4 * (q4 >> 1) + (s4 >> 2)) * MM_VST + 2 * (32 * db + 16 * (q4 & 1) + 4 * (s4 & 3));
+                const pa_h4 x0 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) vb));
+                const pa_h4 x1 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vb + 8 * MM_VST)));
+                const mm_h8 va = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+                O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, P[mi], O[db], 0, 0, 0);
+            }
+        }
+        mm_lds_barrier();                                            // this stage is free; the next one is written
+    }
+
+    // ---- row n: the sum over both lanes; O rebased from the reference max to the exact one
+    const float lt = mm_sum32(lsum);
+    const float f = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mx);
+    if (!rlive) return;
+    const bool direct = a.n_chunks == 1 && a.fused;
+    float * dst = direct ? a.O + ((size_t) h * a.rows + row) * MM_HD
+                         : a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row) * MM_HD;
+    #pragma unroll
+    for (int db = 0; db < 4; db++)
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const pa_f4 v = {O[db][4 * j] * f, O[db][4 * j + 1] * f, O[db][4 * j + 2] * f, O[db][4 * j + 3] * f};
+            *(pa_f4 *) (dst + 32 * db + 8 * j + 4 * h2) = v;
+        }
+    if (h2 == 0) {
+        if (direct) {
+            a.m[(size_t) h * a.rows + row] = mx == -INFINITY ? -INFINITY : mx * PA_LN2;
+            a.l[(size_t) h * a.rows + row] = lt * f;
+        } else {
+            a.pml[((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row] = make_float2(mx, lt * f);
+        }
+    }
+}
+
+template <int FMT>
+static hipError_t launch_mma_fmt(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    switch (nw) {
+        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
+        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    if (fmt == 0) return launch_mma_fmt<0>(nw, a, grid, st, ev0, ev1);
+    if (fmt == 1) return launch_mma_fmt<1>(nw, a, grid, st, ev0, ev1);
+    if (fmt == 2) return launch_mma_fmt<2>(nw, a, grid, st, ev0, ev1);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace pa_hip
