@@ -115,7 +115,7 @@ __device__ __forceinline__ float mm_sum32(float v) {    // sum over lanes l and 
 }
 
 template <int FMT, int NW>
-__global__ __launch_bounds__(64 * NW) void mma_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
     constexpr int NT = 64 * NW;
     constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
     static_assert(UPT * NT == 512, "NW must be 2, 4 or 8");
@@ -138,21 +138,37 @@ __global__ __launch_bounds__(64 * NW) void mma_kernel(const AttnArgs a) {
     const uint32_t row = rb * (32 * NW) + 32 * wave + n;             // this lane's query row (within the KV head)
     const bool rlive = row < a.rows;
 
-    // ---- staging units of this thread: u = tid + NT*i -> tensor u >> 8, key (u >> 3) & 31, block (u >> 1) & 3,
-    // half u & 1; rows past the page's end reload its last row (masked later)
+    // ---- page cursors (scalar): the page holding a tile, its tile range and key count; a cursor moves only when a tile
+    // leaves its page, so the common case reads no kernel argument memory (whose scalar loads would also wait for the
+    // LDS operations in flight)
+    struct Cursor { uint32_t pg, tb, te, nk; const uint8_t * kb, * vb; };
+    auto cursor0 = [&]() { return Cursor{0u, a.cstart[0], a.cstart[1], a.pstart[1] - a.pstart[0], a.kp[0], a.vp[0]}; };
+    auto seek = [&](Cursor & cu, uint32_t tau) {
+        while (tau >= cu.te) {
+            cu.pg++;
+            cu.tb = cu.te;
+            cu.te = a.cstart[cu.pg + 1];
+            cu.nk = a.pstart[cu.pg + 1] - a.pstart[cu.pg];
+            cu.kb = a.kp[cu.pg];
+            cu.vb = a.vp[cu.pg];
+            __builtin_amdgcn_s_waitcnt(0xc07f);                      // lgkmcnt(0): no scalar load left outstanding
+        }
+    };
+    Cursor cl = cursor0(), cc = cursor0();                           // the next tile to load / to compute
+
+    // ---- staging units of this thread: u = tid + NT*i -> tensor u >> 8 (= (wave + NW*i) >> 2, uniform), key
+    // (u >> 3) & 31, block (u >> 1) & 3, half u & 1; rows past the page's end reload its last row (masked later)
     using F = MmFmt<FMT>;
     MmRaw<FMT> R[UPT];
-    uint32_t pl = 0, pc = 0;                                         // pages of the next tile to load / to compute
-    auto page_of = [&](uint32_t tau, uint32_t & pg) { while (a.cstart[pg + 1] <= tau) pg++; };
     auto load_tile = [&](uint32_t tau) {
-        page_of(tau, pl);
-        const uint32_t j0 = 32 * (tau - a.cstart[pl]);
-        const uint32_t last = a.pstart[pl + 1] - a.pstart[pl] - 1 - j0;
+        seek(cl, tau);
+        const uint32_t j0 = 32 * (tau - cl.tb);
+        const uint32_t last = cl.nk - 1 - j0;
         #pragma unroll
         for (int i = 0; i < UPT; i++) {
             const int u = tid + NT * i;
-            const int tensor = u >> 8, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
-            const uint8_t * base = (tensor ? a.vp[pl] : a.kp[pl]) + (size_t) h * a.hb;
+            const int tensor = (wave + NW * i) >> 2, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
+            const uint8_t * base = (tensor ? cl.vb : cl.kb) + (size_t) h * a.hb;
             const uint32_t r = j0 + min((uint32_t) key, last);
             mm_load_unit<FMT>(R[i], base + (size_t) r * a.rs + blk * F::BB, half);
         }
@@ -162,7 +178,7 @@ __global__ __launch_bounds__(64 * NW) void mma_kernel(const AttnArgs a) {
         #pragma unroll
         for (int i = 0; i < UPT; i++) {
             const int u = tid + NT * i;
-            const int tensor = u >> 8, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
+            const int tensor = (wave + NW * i) >> 2, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
             pa_u4 lo, hi;
             mm_dequant<FMT>(R[i], half, lo, hi);
             char * dst = tensor ? st + MM_KT + key * MM_VST : st + key * MM_KST;
@@ -235,25 +251,42 @@ __global__ __launch_bounds__(64 * NW) void mma_kernel(const AttnArgs a) {
     float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
     const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit
 
+    const int q4 = lane >> 4, s4 = lane & 15;
     for (uint32_t t = 0; t < ntiles; t++) {
         const int stage = t & 1;
+        const uint32_t tau = t0 + t;
+        seek(cc, tau);                                               // before any LDS operation of this step
+        const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
         // the next tile's bytes -> the other stage (last read before the previous barrier), then the one after's loads
         if (t + 1 < ntiles) {
+            if (t + 2 < ntiles) seek(cl, tau + 2);
             store_tile(stage ^ 1);
-            if (t + 2 < ntiles) load_tile(t0 + t + 2);
+            if (t + 2 < ntiles) load_tile(tau + 2);
         }
-        const uint32_t tau = t0 + t;
-        page_of(tau, pc);
-        const int nvalid = (int) min(32u, a.pstart[pc + 1] - a.pstart[pc] - 32 * (tau - a.cstart[pc]));
         const char * Kt = smem + stage * MM_STAGE;
         const char * Vt = Kt + MM_KT;
 
-        // ---- S^T = K Q'^T
+        // ---- LDS reads: K (A operand of S^T, lane (h2, n): key n, dims 16kk + 8h2 .. +7) first; V^T per dim block
+        // and 16-key half by two transposing reads (lane 16q + s reads key row 16mi + (8 for the second read) +
+        // 4(q >> 1) + s / 4, dims 32db + 16(q & 1) + 4(s % 4) .. +3), which complete under the softmax
+        __builtin_amdgcn_s_waitcnt(0xc07f);                          // lgkmcnt(0): the stores and any scalar load done,
+        mm_h8 kf[8];                                                 // so the MFMAs below wait for their own reads only
+        #pragma unroll
+        for (int kk = 0; kk < 8; kk++) kf[kk] = *(const mm_h8 *) (Kt + n * MM_KST + 32 * kk + 16 * h2);
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- S^T = K Q'^T, each MFMA followed by the two transposing V reads of one (dim block, key half), so that at
+        // most 15 LDS reads are outstanding (the counter's range) and each MFMA waits for its own K read only
         mm_f16 S = (mm_f16){};
+        mm_h8 va[4][2];
         #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
-            const mm_h8 kf = *(const mm_h8 *) (Kt + n * MM_KST + 32 * kk + 16 * h2);
-            S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, Qf[kk], S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], Qf[kk], S, 0, 0, 0);
+            const int db = kk >> 1, mi = kk & 1;
+            const char * vb = Vt + (16 * mi + 4 * (q4 >> 1) + (s4 >> 2)) * MM_VST + 2 * (32 * db + 16 * (q4 & 1) + 4 * (s4 & 3));
+            const pa_h4 x0 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) vb));
+            const pa_h4 x1 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vb + 8 * MM_VST)));
+            va[db][mi] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (nvalid < 32) {                                           // keys 8j + 4h2 + i past the page's end
             #pragma unroll
@@ -263,7 +296,7 @@ __global__ __launch_bounds__(64 * NW) void mma_kernel(const AttnArgs a) {
         float tm = S[0];
         #pragma unroll
         for (int v = 1; v < 16; v++) tm = fmaxf(tm, S[v]);
-        tm = mm_max32(tm) * sm;                   // row n's tile max, base 2
+        tm = mm_max32(tm) * sm;                                      // row n's tile max, base 2
         if (__builtin_amdgcn_ballot_w64(tm > mref + MM_PMAX)) {
             // rare: move the reference max of every row that needs it (uniform branch)
             const float mn = fmaxf(mref, tm);
@@ -286,20 +319,11 @@ __global__ __launch_bounds__(64 * NW) void mma_kernel(const AttnArgs a) {
             #pragma unroll
             for (int t8 = 0; t8 < 8; t8++) P[mi][t8] = (_Float16) p[8 * mi + t8];
 
-        // ---- O^T += V^T P^T: per dim block and 16-key half, V^T by two transposing reads (lane 16q + s reads key
-        // row 16mi + (8 for the second read) + 4(q >> 1) + s / 4, dims 32db + 16(q & 1) + 4(s % 4) .. +3)
-        const int q4 = lane >> 4, s4 = lane & 15;
+        // ---- O^T += V^T P^T
         #pragma unroll
-        for (int db = 0; db < 4; db++) {
+        for (int db = 0; db < 4; db++)
             #pragma unroll
-            for (int mi = 0; mi < 2; mi++) {
-                const char * vb = Vt + (16 * mi + 4 * (q4 >> 1) + (s4 >> 2)) * MM_VST + 2 * (32 * db + 16 * (q4 & 1) + 4 * (s4 & 3));
-                const pa_h4 x0 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) vb));
-                const pa_h4 x1 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vb + 8 * MM_VST)));
-                const mm_h8 va = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
-                O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, P[mi], O[db], 0, 0, 0);
-            }
-        }
+            for (int mi = 0; mi < 2; mi++) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][mi], P[mi], O[db], 0, 0, 0);
         mm_lds_barrier();                                            // this stage is free; the next one is written
     }
 
