@@ -135,6 +135,14 @@ def synth() -> C.CDLL:
     L.pa_synth_event_ms.argtypes = [vp, vp]
     L.pa_synth_event_free.restype = C.c_int
     L.pa_synth_event_free.argtypes = [vp]
+    L.pa_synth_capture_begin.restype = C.c_int
+    L.pa_synth_capture_begin.argtypes = [vp]
+    L.pa_synth_capture_end.restype = vp
+    L.pa_synth_capture_end.argtypes = [vp]
+    L.pa_synth_graph_launch.restype = C.c_int
+    L.pa_synth_graph_launch.argtypes = [vp, vp]
+    L.pa_synth_graph_free.restype = C.c_int
+    L.pa_synth_graph_free.argtypes = [vp]
     _synth = L
     return L
 

@@ -553,6 +553,47 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     }
 }
 
+// Many slots (split-K decode): one workgroup per (row, 32 dims), 8 slot groups x 32 dims per workgroup, so that the
+// grid covers the chip and each slot row's 32 dims are one coalesced 128-byte read.
+template <int HD>
+__global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
+    constexpr int NQ = HD / 32;
+    __shared__ float redm[256];
+    __shared__ float red[8][32];
+    __shared__ float redl[8];
+    const uint32_t r = blockIdx.x / NQ, dq = blockIdx.x % NQ;   // output row h*rows + i, dims 32 dq .. +31
+    const uint32_t h = r / a.rows, i = r % a.rows;
+    const int t = threadIdx.x, d = t % 32, sg = t / 32;
+    const size_t stride = (size_t) a.nkv * a.qr;
+    const size_t pr = (size_t) h * a.qr + i;
+    float M = -INFINITY;
+    for (uint32_t s = t; s < a.n_slots; s += 256) M = fmaxf(M, a.pml[s * stride + pr].x);
+    redm[t] = M;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (t < off) redm[t] = fmaxf(redm[t], redm[t + off]);
+        __syncthreads();
+    }
+    M = redm[0];
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    float acc = 0.0f, L = 0.0f;
+    for (uint32_t s = sg; s < a.n_slots; s += 8) {
+        const float2 ml = a.pml[s * stride + pr];
+        const float w = __builtin_amdgcn_exp2f(ml.x - Ms);          // ml.x = -inf -> 0 (an empty slot)
+        acc += w * a.po[(s * stride + pr) * HD + 32 * dq + d];
+        L += w * ml.y;
+    }
+    red[sg][d] = acc;
+    if (d == 0) redl[sg] = L;
+    __syncthreads();
+    if (sg == 0) {
+        #pragma unroll
+        for (int q = 1; q < 8; q++) { acc += red[q][d]; if (d == 0) L += redl[q]; }
+        a.O[(size_t) r * HD + 32 * dq + d] = acc;
+        if (dq == 0 && d == 0) { a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[r] = L; }
+    }
+}
+
 // ---------------------------------------------------------------- device quantizers
 // ggml quantize_row_q8_0_ref / quantize_row_q4_0_ref, one thread per 32-block. Every float expression rounds as written
 // (no FMA contraction), as the oracle's C restatement does.
@@ -648,6 +689,12 @@ void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
 
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
     const uint32_t grid = a.nkv * a.rows;
+    if (a.n_slots >= 64 && grid < 1024) {                           // few rows, many slots: split the dims too
+        if (hd == 128) hipLaunchKernelGGL(merge_wide_kernel<128>, dim3(grid * 4), dim3(256), 0, st, a);
+        else if (hd == 256) hipLaunchKernelGGL(merge_wide_kernel<256>, dim3(grid * 8), dim3(256), 0, st, a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     if (hd == 128) hipLaunchKernelGGL(merge_kernel<128>, dim3(grid), dim3(256), 0, st, a);
     else if (hd == 256) hipLaunchKernelGGL(merge_kernel<256>, dim3(grid), dim3(256), 0, st, a);
     else return hipErrorInvalidValue;

@@ -156,5 +156,19 @@ float pa_synth_event_ms(void * a, void * b) {
     return hipEventElapsedTime(&ms, (hipEvent_t) a, (hipEvent_t) b) == hipSuccess ? ms : -1.0f;
 }
 int pa_synth_event_free(void * e) { return hipEventDestroy((hipEvent_t) e) == hipSuccess ? 0 : -1; }
+// HIP graphs: capture the work a caller enqueues on a stream, then replay it with one launch
+int pa_synth_capture_begin(void * s) {
+    return hipStreamBeginCapture((hipStream_t) s, hipStreamCaptureModeThreadLocal) == hipSuccess ? 0 : -1;
+}
+void * pa_synth_capture_end(void * s) {   // the instantiated graph, or null
+    hipGraph_t g = nullptr;
+    hipGraphExec_t x = nullptr;
+    if (hipStreamEndCapture((hipStream_t) s, &g) != hipSuccess || !g) return nullptr;
+    const bool ok = hipGraphInstantiate(&x, g, nullptr, nullptr, 0) == hipSuccess;
+    (void) hipGraphDestroy(g);
+    return ok ? (void *) x : nullptr;
+}
+int pa_synth_graph_launch(void * x, void * s) { return hipGraphLaunch((hipGraphExec_t) x, (hipStream_t) s) == hipSuccess ? 0 : -1; }
+int pa_synth_graph_free(void * x) { return hipGraphExecDestroy((hipGraphExec_t) x) == hipSuccess ? 0 : -1; }
 
 }  // extern "C"

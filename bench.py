@@ -7,7 +7,8 @@ query heads over 8 KV heads (GQA 8), head dim 128, 131,072 old q8_0 positions in
 outlier channels per head, 64 distinct seeded caches (18.25 GB in HBM, made on the device by libpa_synth). A step is
 one pass over the 64 layers: per layer one pa_hip_attn call (split-K attention kernel + merge kernel) on one stream.
 
-Printed: ONE JSON line. value = microseconds per layer of the whole call sequence (lower is better); roofline = the
+Printed: ONE JSON line. value = microseconds per layer of the whole call sequence (lower is better), the 64 layers
+captured once as a HIP graph and replayed per step (the eager per-call figure is reported beside it); roofline = the
 decode kernel's algorithmic bytes per launch / its mean duration (start/end events recorded by the kernel launch itself,
 on its stream), traffic = HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
 cpu_baseline = the oracle's ggml-faithful restatement (oracle/pa_oracle.c, OpenMP over rows) timed on this host's cores
@@ -122,6 +123,37 @@ def time_layers(bb, ws, lay: Layers, steps: int, warmup: int):
     return total_ms, kern, wall
 
 
+def time_layers_graph(bb, ws, lay: Layers, steps: int):
+    """The layer sequence captured once as a HIP graph (one pa_hip_attn per layer, its kernels in stream order), then
+    K timed replays: per-layer time without the host's per-launch overhead. Returns total ms, or None if the capture
+    failed."""
+    syn = bb.synth()
+    stream = syn.pa_synth_stream_new()
+    for L in range(lay.n_layers):                                   # sizes the workspace before the capture
+        ws.attn(lay.shape, lay.pages[L], lay.q[L].ptr, lay.O, lay.m, lay.l, stream)
+    syn.pa_synth_stream_sync(stream)
+    if syn.pa_synth_capture_begin(stream) != 0:
+        return None
+    for L in range(lay.n_layers):
+        ws.attn(lay.shape, lay.pages[L], lay.q[L].ptr, lay.O, lay.m, lay.l, stream)
+    gx = syn.pa_synth_capture_end(stream)
+    if not gx:
+        return None
+    syn.pa_synth_graph_launch(gx, stream)
+    syn.pa_synth_stream_sync(stream)
+    e0, e1 = syn.pa_synth_event_new(), syn.pa_synth_event_new()
+    syn.pa_synth_event_record(e0, stream)
+    for _ in range(steps):
+        if syn.pa_synth_graph_launch(gx, stream) != 0:
+            raise RuntimeError("graph launch failed")
+    syn.pa_synth_event_record(e1, stream)
+    syn.pa_synth_stream_sync(stream)
+    total_ms = syn.pa_synth_event_ms(e0, e1)
+    syn.pa_synth_event_free(e0); syn.pa_synth_event_free(e1)
+    syn.pa_synth_graph_free(gx)
+    return total_ms
+
+
 def measured_copy_bw(bb, nbytes=2 << 30):
     """Plain device-to-device copy and read-only stream of nbytes: the achievable-bandwidth reference."""
     syn = bb.synth()
@@ -232,6 +264,12 @@ def main():
 
     lay, head, total_ms, kern = run_config(bb, ws, bb.FMT_Q8_0, args.layers, 131072, 8, args.steps, args.warmup,
                                            "decode 1 token x 64 q-heads / 8 kv-heads, hd 128, 131072 q8_0 keys, 64 layers")
+    g_ms = time_layers_graph(bb, ws, lay, args.steps)
+    head["us_per_layer_eager"] = head["us_per_layer"]
+    if g_ms is not None:                                            # the 64-layer sequence as one graph per step
+        head["us_per_layer"] = round(g_ms * 1e3 / (args.steps * args.layers), 3)
+        total_ms = g_ms
+    head["graph"] = g_ms is not None
     log("headline", json.dumps(head))
     cpu, parity = (None, None) if args.no_cpu else cpu_baseline(bb, lay, max(1, min(args.cpu_layers, args.layers)))
     lay.close()
@@ -267,6 +305,8 @@ def main():
                      "kernel": "pa_hip::dec_kernel<1> (q8_0 decode)", "alg_bytes_per_launch": alg,
                      "kernel_us_mean": round(kmean_s * 1e6, 3)},
         "hbm_frac_call": round(alg / (head["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "timing": {"value_from": "HIP graph of the 64-layer sequence, replayed per step" if head["graph"] else "eager launches",
+                   "us_per_layer_eager": head["us_per_layer_eager"], "attn_kernel_us_p90": head["attn_kernel_us_p90"]},
         "measured_bw_gbs": {k: round(v, 1) for k, v in bw.items()},
         "cpu_baseline": cpu, "parity_vs_cpu": parity,
     }

@@ -78,18 +78,28 @@ def test_empty(ws, rows):
     assert np.all(O == 0) and np.all(np.isneginf(m)) and np.all(l == 0)
 
 
-def test_chunking_invariance(ws):
-    """Split-K chunking and the fold change the result only by where P is rounded to fp16 (relative to a different
-    running max): l and m agree to fp32 reordering, O within the P rounding (~2^-11 per weight)."""
-    K, V, Q, rs = case(bb.FMT_Q8_0, 2, 8, 128, 5000, 77)
-    shape = bb.make_shape(2, 8, 128, bb.FMT_Q8_0, rs=rs)
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0])
+def test_split_invariance(ws, fmt):
+    """Splitting the keys over tile groups (split-K slots, folded by the merge kernel or in-kernel by the last
+    workgroups, one or two levels) changes the result only by where P is rounded to fp16 (relative to a different
+    running max): l and m agree to fp32 reordering, O within the P rounding (~2^-11 per weight); every split is also
+    within the parity bar of the oracle."""
+    K, V, Q, rs = case(fmt, 2, 8, 128, 5000, 77)            # pages of 1500 keys: 157 tiles
+    shape = bb.make_shape(2, 8, 128, fmt, rs=rs)
+    ref = orc.attn_ggml(orc.make_shape(2, 8, 128, fmt, orc.QMODE_GGML, rs=rs), Q, K, V, 5000)
     outs = []
-    for chunk in ("256", "512", "1024", "4096", "8192"):
-        os.environ["PA_HIP_CHUNK"] = chunk
+    for env in ({"PA_HIP_GROUPS": "1"}, {"PA_HIP_GROUPS": "3"}, {"PA_HIP_GROUPS": "40"}, {"PA_HIP_GROUPS": "157"},
+                {"PA_HIP_GROUPS": "17", "PA_HIP_DEC_FOLD": "1"}, {"PA_HIP_GROUPS": "40", "PA_HIP_DEC_FOLD": "1"},
+                {"PA_HIP_GROUPS": "157", "PA_HIP_DEC_FOLD": "1"}):
+        print("split", env, flush=True)
+        os.environ.update(env)
         try:
             outs.append(bb.attn_host(shape, K, V, Q, page_keys=1500, ws=ws))
         finally:
-            del os.environ["PA_HIP_CHUNK"]
+            for k in env:
+                del os.environ[k]
+        eo, em, el = orc.rel_err(*outs[-1], *ref)
+        assert eo < TOL and em < TOL and el < TOL, (env, eo, em, el)
     for O, m, l in outs[1:]:
         eo, em, el = orc.rel_err(O, m, l, *outs[0])
         assert eo < 1e-3 and em < 1e-6 and el < 1e-5, (eo, em, el)
