@@ -162,6 +162,20 @@ bool launch_fold(pa_hip_ws * ws, uint32_t n_slots, uint32_t nkv, uint32_t qr, ui
 int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
                 const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
     const uint32_t qr = 8, tile = 32;
+    // pages above 2^20 keys are split (the kernel's per-tile buffer ranges are 32-bit byte counts)
+    std::vector<const void *> kpx, vpx;
+    std::vector<uint32_t> nkx;
+    for (int i = 0; i < n_pages; i++) {
+        uint32_t done = 0;
+        do {
+            const uint32_t c = std::min<uint32_t>(nkeys[i] - done, 1u << 20);
+            kpx.push_back((const uint8_t *) k_pages[i] + (size_t) done * s->rs);
+            vpx.push_back((const uint8_t *) v_pages[i] + (size_t) done * s->rs);
+            nkx.push_back(c);
+            done += c;
+        } while (done < nkeys[i]);
+    }
+    k_pages = kpx.data(); v_pages = vpx.data(); nkeys = nkx.data(); n_pages = (int) nkx.size();
     // groups of tiles per head pair (group c takes the tiles c, c + G, ...): about PA_HIP_TARGET_WG workgroups in all
     const int target = std::max(1, env_int("PA_HIP_TARGET_WG", 1024));
     const int forced_groups = env_int("PA_HIP_GROUPS", 0);

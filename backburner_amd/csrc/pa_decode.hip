@@ -51,7 +51,8 @@ constexpr int DEC_PBLK = 32 * 16;         // LDS bytes of one P' block: [32 keys
 constexpr int DEC_QBLK = 8 * 32 + 16;     // LDS bytes of one query block table: [8 rows][2 halves][16 bytes] + zero slot
 constexpr int DEC_WLDS = 32 * DEC_VST + DEC_NKB * DEC_PBLK + DEC_NKB * DEC_QBLK + 2 * DEC_NKB * 8 * 4;
                                           // per wave: V tile, P' tiles, query tables, query scales + q4_0 sums
-constexpr float PMAX_LOG2 = 6.0f;         // p <= 2^6 between rescales (P' = p * d_v stays finite for |d_v| < 1023)
+constexpr float PMAX_LOG2 = 6.0f;
+constexpr int DEC_PF = 2;                 // tiles whose raw bytes are in flight in registers per wave (3 measured no faster)         // p <= 2^6 between rescales (P' = p * d_v stays finite for |d_v| < 1023)
 
 template <int FMT> struct DecGeom {
     static constexpr int BB = FMT == 1 ? 34 : 18;          // bytes per quant block
@@ -225,23 +226,21 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     char * Qt = Pl + DEC_NKB * DEC_PBLK;                             // [NKB][DEC_QBLK] int8 query operands
     float * Ct = (float *) (Qt + DEC_NKB * DEC_QBLK);                // [NKB][8] scales, then [NKB][8] q4_0 starts
 
-    // ---- tile loads: wave 0 loads K, wave 1 V; chunk q = 64 i + lane is key q / NCH, bytes 16 * (q % NCH) of the pair
-    // slice; rows past the page's end reload its last row (masked later)
-    uint32_t qkey[CPL], qoff[CPL];
+    // ---- tile loads: wave 0 loads K, wave 1 V, as buffer loads from a per-tile scalar base (the tile's first row of
+    // the pair slice) whose range ends with the page: chunk q = 64 i + lane is key q / NCH, bytes 16 * (q % NCH) of the
+    // slice; rows past the page's end, and lanes past the tile's chunks, read zeros (range check, no memory access)
+    uint32_t vo[CPL];
     #pragma unroll
     for (int i = 0; i < CPL; i++) {
-        const int q = min(64 * i + lane, TCH - 1);                   // a lane past the tile's chunks reloads the last
-        qkey[i] = (uint32_t) (q / G::NCH);
-        qoff[i] = 16u * (uint32_t) (q % G::NCH);
+        const int q = 64 * i + lane;
+        vo[i] = q < TCH ? (uint32_t) (q / G::NCH) * rs + 16u * (uint32_t) (q % G::NCH) : 0x80000000u;
     }
     auto page_of = [&](uint32_t tau, uint32_t & pg) { while (a.cstart[pg + 1] <= tau) pg++; };   // pages only advance
-    auto tile_load = [&](pa_u4 (&X)[CPL], uint32_t pg, uint32_t j0, uint32_t last) {   // rows j0 + min(key, last)
-        const uint8_t * tb = (hd ? a.vp[pg] : a.kp[pg]) + (size_t) pr * G::SL;
+    auto tile_load = [&](pa_u4 (&X)[CPL], uint32_t pg, uint32_t j0, uint32_t nrec) {   // rows j0 .. of page pg
+        const uint8_t * tb = (hd ? a.vp[pg] : a.kp[pg]) + (size_t) pr * G::SL + (size_t) j0 * rs;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *) tb, (short) 0, (int) nrec, 0x00020000);
         #pragma unroll
-        for (int i = 0; i < CPL; i++) {
-            const uint32_t row = j0 + min(qkey[i], last);
-            X[i] = pa_ld<pa_u4>(tb + (size_t) row * rs + qoff[i]);
-        }
+        for (int i = 0; i < CPL; i++) X[i] = __builtin_bit_cast(pa_u4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, vo[i], 0, 0));
     };
     auto tile_store = [&](const pa_u4 (&X)[CPL]) {
         char * dst = raw + hd * TCH * 16 + 16 * lane;
@@ -267,19 +266,23 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t ntiles = (T - c + NG - 1) / NG;                   // >= 1: c < NG <= T
     uint32_t pl = 0, pc = 0;                                         // pages of the next tile to load / to compute
-    auto load_tile = [&](pa_u4 (&X)[CPL], uint32_t tau) {            // tile tau, or a cheap dummy (one row) past the end
+    auto load_tile = [&](pa_u4 (&X)[CPL], uint32_t tau) {            // tile tau, or (past the end) an empty range
         if (tau < T) {
             page_of(tau, pl);
             const uint32_t j0 = 32 * (tau - a.cstart[pl]);
-            tile_load(X, pl, j0, a.pstart[pl + 1] - a.pstart[pl] - 1 - j0);
+            tile_load(X, pl, j0, (a.pstart[pl + 1] - a.pstart[pl] - j0) * rs - pr * G::SL);
         } else {
-            tile_load(X, pl, 0, 0);
+            tile_load(X, pl, 0, 0u);
         }
     };
-    pa_u4 X0[CPL], X1[CPL];                                          // tiles c, c + 2 NG, ... and c + NG, c + 3 NG, ...
+    // DEC_PF register sets: tile c + k NG in set k % DEC_PF, each set's batch issued strictly after the previous
+    // set's (in-order counters: the wait before a tile covers only its own batch)
+    pa_u4 X0[CPL], X1[CPL], X2[CPL];
     load_tile(X0, c);
-    __builtin_amdgcn_sched_barrier(0);                               // X0's loads strictly before X1's (in-order counts)
+    __builtin_amdgcn_sched_barrier(0);
     load_tile(X1, c + NG);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DEC_PF == 3) load_tile(X2, c + 2 * NG);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- query rows: ggml's q8_0 of each 32-block (d = amax/127, id = 1/d, q = roundf(x*id), d -> fp16;
@@ -343,13 +346,13 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     uint8_t * vdst = Vs + kap * DEC_VST;
 
     auto tile = [&](pa_u4 (&X)[CPL], uint32_t tau) {
-        // ---- the tile's raw pair slices -> LDS (this wave's tensor), then this register set's next tile (two steps
-        // ahead; past the last one a dummy load that nothing reads)
+        // ---- the tile's raw pair slices -> LDS (this wave's tensor), then this register set's next tile (DEC_PF steps
+        // ahead; past the last one an empty range that loads nothing)
         page_of(tau, pc);
         const int nvalid = (int) min(32u, a.pstart[pc + 1] - a.pstart[pc] - 32 * (tau - a.cstart[pc]));
         dec_lds_barrier();                                           // both waves are done reading the previous tile
         tile_store(X);
-        load_tile(X, tau + 2 * NG);
+        load_tile(X, tau + DEC_PF * NG);
         dec_lds_barrier();                                           // the tile's raw bytes are visible
         __builtin_amdgcn_sched_barrier(0);
 
@@ -451,15 +454,18 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         dec_wave_sync();
     };
-    // pairs of tiles, then an odd last one: no exit between the two halves, so the load order (X0's batch before X1's)
-    // is the same on every path into a tile and the wait before each tile covers only its own batch
+    // groups of DEC_PF tiles, then the rest: no exit inside a group, so the load order (X0's batch, X1's, ...) is the
+    // same on every path into a tile and the wait before each tile covers only its own batch
     uint32_t tau = c;
-    for (uint32_t t = 0; t + 1 < ntiles; t += 2) {
+    uint32_t t = 0;
+    for (; t + DEC_PF <= ntiles; t += DEC_PF) {
         tile(X0, tau);
         tile(X1, tau + NG);
-        tau += 2 * NG;
+        if constexpr (DEC_PF == 3) tile(X2, tau + 2 * NG);
+        tau += DEC_PF * NG;
     }
-    if (ntiles & 1) tile(X0, tau);
+    if (t < ntiles) tile(X0, tau);
+    if (t + 1 < ntiles) tile(X1, tau + NG);
 
     // ---- this wave's head: rows' (sum, exact max) over the lanes; O rebased from the reference max to the exact one
     // and written from lanes n < 8 (final result for a single group, else the group's split-K slot)
