@@ -51,8 +51,8 @@ constexpr int DEC_PBLK = 32 * 16;         // LDS bytes of one P' block: [32 keys
 constexpr int DEC_QBLK = 8 * 32 + 16;     // LDS bytes of one query block table: [8 rows][2 halves][16 bytes] + zero slot
 constexpr int DEC_WLDS = 32 * DEC_VST + DEC_NKB * DEC_PBLK + DEC_NKB * DEC_QBLK + 2 * DEC_NKB * 8 * 4;
                                           // per wave: V tile, P' tiles, query tables, query scales + q4_0 sums
-constexpr float PMAX_LOG2 = 6.0f;
-constexpr int DEC_PF = 2;                 // tiles whose raw bytes are in flight in registers per wave (3 measured no faster)         // p <= 2^6 between rescales (P' = p * d_v stays finite for |d_v| < 1023)
+constexpr float PMAX_LOG2 = 6.0f;         // p <= 2^6 between rescales (P' = p * d_v stays finite for |d_v| < 1023)
+constexpr int DEC_PF = 2;                 // tiles whose raw bytes are in flight in registers per wave (3: no faster)
 
 template <int FMT> struct DecGeom {
     static constexpr int BB = FMT == 1 ? 34 : 18;          // bytes per quant block
