@@ -553,44 +553,65 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     }
 }
 
-// Many slots (split-K decode): one workgroup per (row, 32 dims), 8 slot groups x 32 dims per workgroup, so that the
-// grid covers the chip and each slot row's 32 dims are one coalesced 128-byte read.
+// Many slots (split-K decode, up to 256): one workgroup per (row, 32 dims), one thread per slot, so that every load
+// of the fold is issued at once (one memory latency, not one per slot): thread t reads slot t's (max, sum) and its 32
+// dims, the workgroup reduces the max and the weighted sums through LDS.
 template <int HD>
 __global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
     constexpr int NQ = HD / 32;
-    __shared__ float redm[256];
-    __shared__ float red[8][32];
-    __shared__ float redl[8];
+    __shared__ float sO[256][33];                   // slot x dim (padded: column sums read conflict-free)
+    __shared__ float sP[8][32];
+    __shared__ float sM[4], sL[4];
     const uint32_t r = blockIdx.x / NQ, dq = blockIdx.x % NQ;   // output row h*rows + i, dims 32 dq .. +31
     const uint32_t h = r / a.rows, i = r % a.rows;
-    const int t = threadIdx.x, d = t % 32, sg = t / 32;
+    const int t = threadIdx.x, lane = t % 64, wv = t / 64;
     const size_t stride = (size_t) a.nkv * a.qr;
     const size_t pr = (size_t) h * a.qr + i;
-    float M = -INFINITY;
-    for (uint32_t s = t; s < a.n_slots; s += 256) M = fmaxf(M, a.pml[s * stride + pr].x);
-    redm[t] = M;
-    __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (t < off) redm[t] = fmaxf(redm[t], redm[t + off]);
-        __syncthreads();
-    }
-    M = redm[0];
-    const float Ms = M == -INFINITY ? 0.0f : M;
-    float acc = 0.0f, L = 0.0f;
-    for (uint32_t s = sg; s < a.n_slots; s += 8) {
-        const float2 ml = a.pml[s * stride + pr];
-        const float w = __builtin_amdgcn_exp2f(ml.x - Ms);          // ml.x = -inf -> 0 (an empty slot)
-        acc += w * a.po[(s * stride + pr) * HD + 32 * dq + d];
-        L += w * ml.y;
-    }
-    red[sg][d] = acc;
-    if (d == 0) redl[sg] = L;
-    __syncthreads();
-    if (sg == 0) {
+    const bool live = (uint32_t) t < a.n_slots;
+    float2 ml = make_float2(-INFINITY, 0.0f);
+    pa_f4 o[8];
+    if (live) {
+        ml = a.pml[t * stride + pr];
         #pragma unroll
-        for (int q = 1; q < 8; q++) { acc += red[q][d]; if (d == 0) L += redl[q]; }
-        a.O[(size_t) r * HD + 32 * dq + d] = acc;
-        if (dq == 0 && d == 0) { a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[r] = L; }
+        for (int j = 0; j < 8; j++) o[j] = *(const pa_f4 *) (a.po + (t * stride + pr) * HD + 32 * dq + 4 * j);
+    } else {
+        #pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = (pa_f4){0.f, 0.f, 0.f, 0.f};
+    }
+    float M = ml.x;
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) sM[wv] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(sM[0], sM[1]), fmaxf(sM[2], sM[3]));
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    const float w = __builtin_amdgcn_exp2f(ml.x - Ms);              // -inf (an empty or absent slot) -> 0
+    float L = w * ml.y;
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+    if (lane == 0) sL[wv] = L;
+    #pragma unroll
+    for (int j = 0; j < 8; j++)
+        #pragma unroll
+        for (int k = 0; k < 4; k++) sO[t][4 * j + k] = w * o[j][k];
+    __syncthreads();
+    {                                                                // column sums over 8 segments of 32 slots
+        const int c = t % 32, seg = t / 32;
+        float acc = 0.0f;
+        #pragma unroll
+        for (int q = 0; q < 32; q++) acc += sO[32 * seg + q][c];
+        sP[seg][c] = acc;
+    }
+    __syncthreads();
+    if (t < 32) {
+        float acc = 0.0f;
+        #pragma unroll
+        for (int seg = 0; seg < 8; seg++) acc += sP[seg][t];
+        a.O[(size_t) r * HD + 32 * dq + t] = acc;
+        if (dq == 0 && t == 0) {
+            a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2;
+            a.l[r] = sL[0] + sL[1] + sL[2] + sL[3];
+        }
     }
 }
 
@@ -689,7 +710,7 @@ void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
 
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
     const uint32_t grid = a.nkv * a.rows;
-    if (a.n_slots >= 64 && grid < 1024) {                           // few rows, many slots: split the dims too
+    if (a.n_slots >= 64 && a.n_slots <= 256 && grid < 1024) {       // few rows, many slots: one thread per slot
         if (hd == 128) hipLaunchKernelGGL(merge_wide_kernel<128>, dim3(grid * 4), dim3(256), 0, st, a);
         else if (hd == 256) hipLaunchKernelGGL(merge_wide_kernel<256>, dim3(grid * 8), dim3(256), 0, st, a);
         else return hipErrorInvalidValue;
