@@ -615,6 +615,45 @@ __global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
     }
 }
 
+// Few slots (prefill, up to 16): 256 / (HD / 4) rows per workgroup, HD / 4 threads per row (4 dims each), every
+// slot's load issued at once.
+template <int HD>
+__global__ __launch_bounds__(256) void merge_rows_kernel(const MergeArgs a) {
+    constexpr int TPR = HD / 4, RPW = 256 / TPR, MS = 16;
+    const int t = threadIdx.x, d4 = t % TPR;
+    const uint32_t r = blockIdx.x * RPW + t / TPR;                   // output row h*rows + i
+    if (r >= a.nkv * a.rows) return;
+    const uint32_t h = r / a.rows, i = r % a.rows;
+    const size_t stride = (size_t) a.nkv * a.qr;
+    const size_t pr = (size_t) h * a.qr + i;
+    float2 ml[MS];
+    pa_f4 o[MS];
+    #pragma unroll
+    for (int s = 0; s < MS; s++) {
+        if ((uint32_t) s < a.n_slots) {
+            ml[s] = a.pml[s * stride + pr];
+            o[s] = *(const pa_f4 *) (a.po + (s * stride + pr) * HD + 4 * d4);
+        } else {
+            ml[s] = make_float2(-INFINITY, 0.0f);
+            o[s] = (pa_f4){0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    float M = -INFINITY;
+    #pragma unroll
+    for (int s = 0; s < MS; s++) M = fmaxf(M, ml[s].x);
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.0f;
+    #pragma unroll
+    for (int s = 0; s < MS; s++) {
+        const float w = __builtin_amdgcn_exp2f(ml[s].x - Ms);       // -inf (an empty or absent slot) -> 0
+        acc += w * o[s];
+        L += w * ml[s].y;
+    }
+    *(pa_f4 *) (a.O + (size_t) r * HD + 4 * d4) = acc;
+    if (d4 == 0) { a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[r] = L; }
+}
+
 // ---------------------------------------------------------------- device quantizers
 // ggml quantize_row_q8_0_ref / quantize_row_q4_0_ref, one thread per 32-block. Every float expression rounds as written
 // (no FMA contraction), as the oracle's C restatement does.
@@ -710,9 +749,15 @@ void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
 
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
     const uint32_t grid = a.nkv * a.rows;
-    if (a.n_slots >= 64 && a.n_slots <= 256 && grid < 1024) {       // few rows, many slots: one thread per slot
+    if (a.n_slots >= 32 && a.n_slots <= 256) {                      // many slots: one thread per slot
         if (hd == 128) hipLaunchKernelGGL(merge_wide_kernel<128>, dim3(grid * 4), dim3(256), 0, st, a);
         else if (hd == 256) hipLaunchKernelGGL(merge_wide_kernel<256>, dim3(grid * 8), dim3(256), 0, st, a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
+    if (a.n_slots <= 16) {                                           // few slots: several rows per workgroup
+        if (hd == 128) hipLaunchKernelGGL(merge_rows_kernel<128>, dim3((grid + 7) / 8), dim3(256), 0, st, a);
+        else if (hd == 256) hipLaunchKernelGGL(merge_rows_kernel<256>, dim3((grid + 3) / 4), dim3(256), 0, st, a);
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }
