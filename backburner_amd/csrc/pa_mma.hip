@@ -12,10 +12,11 @@
 // and sum need one exchange with lane n + 32 per tile and no LDS.
 //
 // Q' is the query as fp16: PA_QMODE_GGML converts Q to K's vec_dot type as ggml's CPU flash_attn_ext does - q8_0 per
-// 32-block for quantized K (quantize_row_q8_0_ref), taken as fp16(d*q*scale), and fp16(q) for f16 K (the scale then
-// multiplies the score); PA_QMODE_F16 takes fp16(q*scale) (the reference engines' Qs, phone-attn.h:595-599). Online softmax in base 2 with a
-// reference max that moves only when a score exceeds it by more than 2^MM_PMAX (O is rescaled rarely); the exact max
-// is tracked beside it and applied at the end. Output: one split-K slot per workgroup (O unnormalised against the
+// 32-block for quantized K (quantize_row_q8_0_ref), taken as fp16(d*q*scale*log2 e) so the scores come out in base-2
+// units, and fp16(q) for f16 K (the scale then multiplies the score); PA_QMODE_F16 takes fp16(q*scale) (the reference
+// engines' Qs, phone-attn.h:595-599). Online softmax in base 2 with a reference max that moves only when a score
+// exceeds it by more than 2^MM_PMAX (O is rescaled rarely); the exact max is tracked beside it and applied at the end.
+// The row sum adds the fp16 probabilities the PV MFMAs consume. Output: one split-K slot per workgroup (O unnormalised against the
 // base-2 max, max, sum), folded by merge_kernel, or the final (O, m, l) when the call has a single chunk.
 //
 // Reference roles: pa_attn_big + pa_big_load (pa-metal.mm:379-487: per (row tile, KV head, key chunk) dequantize a
@@ -114,7 +115,10 @@ __device__ __forceinline__ float mm_sum32(float v) {    // sum over lanes l and 
     return __builtin_bit_cast(float, (unsigned) t[0]) + __builtin_bit_cast(float, (unsigned) t[1]);
 }
 
-template <int FMT, int NW>
+// PRE: PA_QMODE_GGML over quantized K. Q' then carries scale * log2 e inside its one fp16 rounding, and the QK
+// accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
+// single exp2. Otherwise the scores are scaled and shifted by one fma each.
+template <int FMT, int NW, bool PRE>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
     constexpr int NT = 64 * NW;
     constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
@@ -202,7 +206,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             x[2 * kk + 1] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 16 * kk + 4)) & qmask);
         }
         const float scale = a.scale;
-        if (a.qmode == 0 && FMT != 0) {                              // PA_QMODE_GGML, quantized K: Q -> q8_0
+        if constexpr (PRE) {                                         // PA_QMODE_GGML, quantized K: Q -> q8_0
             // ggml q8_0 per 32-block b = k-steps 2b, 2b+1: this lane holds 16 of its values, lane ^ 32 the other 16
             #pragma clang fp contract(off)
             #pragma unroll
@@ -216,7 +220,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
                 am = mm_max32(am);
                 const float d = am / 127.0f;
                 const float id = d != 0.0f ? 1.0f / d : 0.0f;
-                const float dq = (float) (_Float16) d * scale;        // the fp16 block scale (as ggml stores it) * scale
+                const float dq = (float) (_Float16) d * (scale * MM_LOG2E);   // the fp16 block scale (as ggml stores it)
+                                                                              // * scale, in base-2 units
                 #pragma unroll
                 for (int kq = 0; kq < 2; kq++) {
                     mm_h8 f;
@@ -249,7 +254,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     #pragma unroll
     for (int db = 0; db < 4; db++) O[db] = (mm_f16){};
     float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
-    const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit
+    const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit (!PRE)
+    mm_f16 Cm = (mm_f16){};                                          // PRE: -mc in every element, the QK start value
+    float mc = 0.0f;                                                 // PRE: mref once it is finite (0 before)
+    const mm_h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
 
     const int q4 = lane >> 4, s4 = lane & 15;
     for (uint32_t t = 0; t < ntiles; t++) {
@@ -276,7 +284,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         __builtin_amdgcn_sched_barrier(0);
         // ---- S^T = K Q'^T, each MFMA followed by the two transposing V reads of one (dim block, key half), so that at
         // most 15 LDS reads are outstanding (the counter's range) and each MFMA waits for its own K read only
-        mm_f16 S = (mm_f16){};
+        mm_f16 S = PRE ? Cm : (mm_f16){};
         mm_h8 va[4][2];
         #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
@@ -296,7 +304,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         float tm = S[0];
         #pragma unroll
         for (int v = 1; v < 16; v++) tm = fmaxf(tm, S[v]);
-        tm = mm_max32(tm) * sm;                                      // row n's tile max, base 2
+        tm = PRE ? mm_max32(tm) + mc : mm_max32(tm) * sm;            // row n's tile max, base 2
         if (__builtin_amdgcn_ballot_w64(tm > mref + MM_PMAX)) {
             // rare: move the reference max of every row that needs it (uniform branch)
             const float mn = fmaxf(mref, tm);
@@ -305,19 +313,25 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             for (int db = 0; db < 4; db++) O[db] *= alpha;
             lsum *= alpha;
             mref = mn;
+            if constexpr (PRE) {                                     // rebase this tile's scores and the start value
+                const float dl = mn - mc;
+                #pragma unroll
+                for (int v = 0; v < 16; v++) S[v] -= dl;
+                mc = mn;
+                #pragma unroll
+                for (int v = 0; v < 16; v++) Cm[v] = -mn;
+            }
         }
         mx = fmaxf(mx, tm);
-        float p[16];
-        #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            p[v] = __builtin_amdgcn_exp2f(fmaf(S[v], sm, -mref));
-            lsum += p[v];
-        }
         mm_h8 P[2];
         #pragma unroll
-        for (int mi = 0; mi < 2; mi++)
-            #pragma unroll
-            for (int t8 = 0; t8 < 8; t8++) P[mi][t8] = (_Float16) p[8 * mi + t8];
+        for (int v = 0; v < 16; v++)
+            P[v / 8][v % 8] = (_Float16) __builtin_amdgcn_exp2f(PRE ? S[v] : fmaf(S[v], sm, -mref));
+        #pragma unroll
+        for (int v = 0; v < 16; v += 2) {                            // the row sum of the fp16 P the PV MFMAs use
+            const mm_h2 pp = {P[v / 8][v % 8], P[v / 8][v % 8 + 1]};
+            lsum = __builtin_amdgcn_fdot2(pp, one2, lsum, false);
+        }
 
         // ---- O^T += V^T P^T
         #pragma unroll
@@ -351,21 +365,22 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     }
 }
 
-template <int FMT>
+template <int FMT, bool PRE>
 static hipError_t launch_mma_fmt(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     switch (nw) {
-        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
-        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
+        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
+        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    if (fmt == 0) return launch_mma_fmt<0>(nw, a, grid, st, ev0, ev1);
-    if (fmt == 1) return launch_mma_fmt<1>(nw, a, grid, st, ev0, ev1);
-    if (fmt == 2) return launch_mma_fmt<2>(nw, a, grid, st, ev0, ev1);
+    const bool pre = a.qmode == 0;                                   // PA_QMODE_GGML (over quantized K)
+    if (fmt == 0) return launch_mma_fmt<0, false>(nw, a, grid, st, ev0, ev1);
+    if (fmt == 1) return pre ? launch_mma_fmt<1, true>(nw, a, grid, st, ev0, ev1) : launch_mma_fmt<1, false>(nw, a, grid, st, ev0, ev1);
+    if (fmt == 2) return pre ? launch_mma_fmt<2, true>(nw, a, grid, st, ev0, ev1) : launch_mma_fmt<2, false>(nw, a, grid, st, ev0, ev1);
     return hipErrorInvalidValue;
 }
 
