@@ -91,6 +91,15 @@ def lib() -> C.CDLL:
     L.pa_hip_ws_time_next.argtypes = [vp, vp, vp]
     L.pa_hip_quantize.restype = C.c_int
     L.pa_hip_quantize.argtypes = [C.c_int, vp, vp, C.c_int64, vp]
+    L.pa_hip_attn_reply.restype = C.c_int
+    L.pa_hip_attn_reply.argtypes = [vp, C.POINTER(Shape), C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_uint32), C.c_int, vp, vp,
+                                    vp, vp]
+    L.pa_hip_merge_partial.restype = C.c_int
+    L.pa_hip_merge_partial.argtypes = [vp, vp, vp, vp, vp, vp, C.c_uint64, C.c_uint32, vp]
+    L.pa_hip_normalise.restype = C.c_int
+    L.pa_hip_normalise.argtypes = [vp, vp, vp, C.c_uint64, C.c_uint32, vp, vp, vp]
+    L.pa_hip_coattn_merge.restype = C.c_int
+    L.pa_hip_coattn_merge.argtypes = [vp, vp, vp, vp, vp, C.c_uint64, C.c_uint32, vp, vp, vp]
     _hip = L
     return L
 
@@ -276,6 +285,14 @@ class Workspace:
         nk = (C.c_uint32 * max(n, 1))(*pages.nkeys)
         _check(lib().pa_hip_attn(self.ptr, C.byref(shape), kp, vp, nk, n, Q, O, m, l, stream), "pa_hip_attn")
 
+    def attn_reply(self, shape: Shape, pages: Pages, Q: int, Oh: int, lse: int, stream=None) -> None:
+        """Enqueue pa_hip_attn_reply: the call's reply format (f16 O / l, lse) at the device pointers Oh, lse."""
+        n = len(pages.k)
+        kp = (C.c_void_p * max(n, 1))(*pages.k)
+        vp = (C.c_void_p * max(n, 1))(*pages.v)
+        nk = (C.c_uint32 * max(n, 1))(*pages.nkeys)
+        _check(lib().pa_hip_attn_reply(self.ptr, C.byref(shape), kp, vp, nk, n, Q, Oh, lse, stream), "pa_hip_attn_reply")
+
     def time_next(self, ev_start, ev_end) -> None:
         """Record ev_start / ev_end around the attention kernel of the next attn() call."""
         _check(lib().pa_hip_ws_time_next(self.ptr, ev_start, ev_end), "pa_hip_ws_time_next")
@@ -291,6 +308,19 @@ class Workspace:
 
 def quantize_device(fmt: int, x: int, y: int, n: int, stream=None) -> None:
     _check(lib().pa_hip_quantize(fmt, x, y, n, stream), "pa_hip_quantize")
+
+
+def merge_partial_device(O: int, m: int, l: int, O2: int, m2: int, l2: int, rows: int, hd: int, stream=None) -> None:
+    _check(lib().pa_hip_merge_partial(O, m, l, O2, m2, l2, rows, hd, stream), "pa_hip_merge_partial")
+
+
+def normalise_device(O: int, m: int, l: int, rows: int, hd: int, Oh: int, lse: int, stream=None) -> None:
+    _check(lib().pa_hip_normalise(O, m, l, rows, hd, Oh, lse, stream), "pa_hip_normalise")
+
+
+def coattn_merge_device(Oh: int, lse: int, O_loc: int, m_loc: int, l_loc: int, rows: int, hd: int, out: int, lse_out=None,
+                        stream=None) -> None:
+    _check(lib().pa_hip_coattn_merge(Oh, lse, O_loc, m_loc, l_loc, rows, hd, out, lse_out, stream), "pa_hip_coattn_merge")
 
 
 def make_shape(nkv: int, rows: int, hd: int, fmt: int, qmode: int = QMODE_GGML, scale: float | None = None,

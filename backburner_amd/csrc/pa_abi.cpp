@@ -89,6 +89,12 @@ struct pa_hip_ws {
     float * dout = nullptr; size_t dout_cap = 0;
     // measurement hook (pa_hip_ws_time_next)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    // pa_hip_attn_reply: (O, m, l) staging, and the reply target the split-K merge writes directly when the call has one
+    float * ro = nullptr; size_t ro_cap = 0;
+    float * rml = nullptr; size_t rml_cap = 0;
+    uint16_t * reply_oh = nullptr;
+    float * reply_lse = nullptr;
+    bool reply_done = false;
 };
 
 extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
@@ -108,7 +114,7 @@ extern "C" void pa_hip_ws_destroy(pa_hip_ws * w) {
     if (!w) return;
     (void) hipDeviceSynchronize();
     hipFree(w->ctr); hipFree(w->go); hipFree(w->gml); hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
-    hipFree(w->dk); hipFree(w->dv); hipFree(w->dq); hipFree(w->dout);
+    hipFree(w->dk); hipFree(w->dv); hipFree(w->dq); hipFree(w->dout); hipFree(w->ro); hipFree(w->rml);
     if (w->stream) hipStreamDestroy(w->stream);
     delete w;
 }
@@ -147,12 +153,20 @@ int pick_cfg(uint32_t rows, uint32_t hd) {
     return CFG_PREFILL;
 }
 
+// pa_hip_attn_reply: the merge writes the reply format itself (the caller's (O, m, l) then stay unwritten)
+void reply_target(pa_hip_ws * ws, MergeArgs & ma) {
+    if (!ws->reply_oh) return;
+    ma.Oh = ws->reply_oh; ma.lse = ws->reply_lse;
+    ws->reply_done = true;
+}
+
 // merge the split-K slots of a call into (O, m, l); zero slots write (0, -inf, 0)
 bool launch_fold(pa_hip_ws * ws, uint32_t n_slots, uint32_t nkv, uint32_t qr, uint32_t rows, int hd, float * O, float * m, float * l,
                  hipStream_t st) {
     MergeArgs ma;
     ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
     ma.n_slots = n_slots; ma.nkv = nkv; ma.qr = qr; ma.rows = rows;
+    reply_target(ws, ma);
     return hip_ok(launch_merge(hd, ma, st), "merge launch");
 }
 
@@ -317,6 +331,7 @@ int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_page
         MergeArgs ma;
         ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
         ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        reply_target(ws, ma);
         if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
     }
     return 0;
@@ -412,6 +427,7 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         MergeArgs ma;
         ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
         ma.n_slots = 0; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        reply_target(ws, ma);
         if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
     }
     for (const launch_t & ln : L) {
@@ -439,6 +455,7 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         MergeArgs ma;
         ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
         ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        reply_target(ws, ma);
         if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
     }
     return 0;
@@ -459,6 +476,66 @@ extern "C" int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, i
     a.logits = logits; a.draft = draft; a.out = out; a.part = ws->apart; a.counter = ws->acount;
     a.vocab = vocab; a.n_rows = n_rows; a.splits = splits;
     return hip_ok(launch_accept(a, (hipStream_t) stream), "accept launch") ? 0 : -1;
+}
+
+// ---------------------------------------------------------------- 3. the reply side
+extern "C" int pa_hip_attn_reply(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages,
+                                 const void * const * v_pages, const uint32_t * nkeys, int n_pages, const float * Q,
+                                 uint16_t * Oh, float * lse, void * stream) {
+    if (!ws || !s) { set_err("pa_hip_attn_reply: null workspace or shape"); return -1; }
+    if (!Oh || !lse) { set_err("pa_hip_attn_reply: null Oh/lse"); return -1; }
+    if ((uintptr_t) Oh & 7) { set_err("pa_hip_attn_reply: Oh must be 8-byte aligned"); return -1; }
+    if (s->hd != 128 && s->hd != 256) { set_err("pa_hip_attn_reply: hd must be 128 or 256"); return -1; }
+    const size_t rows = (size_t) s->nkv * s->rows;
+    if (!ensure(ws->ro, ws->ro_cap, std::max<size_t>(rows, 1) * s->hd * sizeof(float), "hipMalloc reply O") ||
+        !ensure(ws->rml, ws->rml_cap, std::max<size_t>(rows, 1) * 2 * sizeof(float), "hipMalloc reply m, l"))
+        return -1;
+    ws->reply_oh = Oh; ws->reply_lse = lse; ws->reply_done = false;
+    const int rc = pa_hip_attn(ws, s, k_pages, v_pages, nkeys, n_pages, Q, ws->ro, ws->rml, ws->rml + rows, stream);
+    const bool done = ws->reply_done;
+    ws->reply_oh = nullptr; ws->reply_lse = nullptr; ws->reply_done = false;
+    if (rc != 0) return rc;
+    if (done) return 0;                                               // the split-K merge wrote the reply
+    // a single-chunk call wrote (O, m, l) directly: normalise them
+    return hip_ok(launch_normalise((int) s->hd, ws->ro, ws->rml, ws->rml + rows, rows, Oh, lse, (hipStream_t) stream),
+                  "normalise launch") ? 0 : -1;
+}
+
+namespace {
+bool rows_ok(const char * fn, uint64_t rows, uint32_t hd) {
+    if (hd != 128 && hd != 256) { set_err(std::string(fn) + ": hd must be 128 or 256"); return false; }
+    if (rows > (1ull << 24)) { set_err(std::string(fn) + ": more than 2^24 rows"); return false; }   // 2^22 workgroups
+    return true;
+}
+bool aligned(const void * p, uintptr_t a) { return ((uintptr_t) p & (a - 1)) == 0; }
+}  // namespace
+
+extern "C" int pa_hip_merge_partial(float * O, float * m, float * l, const float * O2, const float * m2, const float * l2,
+                                    uint64_t rows, uint32_t hd, void * stream) {
+    if (!rows_ok("pa_hip_merge_partial", rows, hd)) return -1;
+    if (rows > 0 && (!O || !m || !l || !O2 || !m2 || !l2)) { set_err("pa_hip_merge_partial: null argument"); return -1; }
+    if (!aligned(O, 16) || !aligned(O2, 16)) { set_err("pa_hip_merge_partial: O, O2 must be 16-byte aligned"); return -1; }
+    return hip_ok(launch_merge_partial((int) hd, O, m, l, O2, m2, l2, rows, (hipStream_t) stream), "merge_partial launch") ? 0 : -1;
+}
+
+extern "C" int pa_hip_normalise(const float * O, const float * m, const float * l, uint64_t rows, uint32_t hd, uint16_t * Oh,
+                                float * lse, void * stream) {
+    if (!rows_ok("pa_hip_normalise", rows, hd)) return -1;
+    if (rows > 0 && (!O || !m || !l || !Oh || !lse)) { set_err("pa_hip_normalise: null argument"); return -1; }
+    if (!aligned(O, 16) || !aligned(Oh, 8)) { set_err("pa_hip_normalise: O must be 16-byte and Oh 8-byte aligned"); return -1; }
+    return hip_ok(launch_normalise((int) hd, O, m, l, rows, Oh, lse, (hipStream_t) stream), "normalise launch") ? 0 : -1;
+}
+
+extern "C" int pa_hip_coattn_merge(const uint16_t * Oh, const float * lse, const float * O_loc, const float * m_loc,
+                                   const float * l_loc, uint64_t rows, uint32_t hd, float * out, float * lse_out, void * stream) {
+    if (!rows_ok("pa_hip_coattn_merge", rows, hd)) return -1;
+    if (rows > 0 && (!Oh || !lse || !O_loc || !m_loc || !l_loc || !out)) { set_err("pa_hip_coattn_merge: null argument"); return -1; }
+    if (!aligned(Oh, 8) || !aligned(O_loc, 16) || !aligned(out, 16)) {
+        set_err("pa_hip_coattn_merge: Oh must be 8-byte, O_loc and out 16-byte aligned");
+        return -1;
+    }
+    return hip_ok(launch_coattn((int) hd, Oh, lse, O_loc, m_loc, l_loc, rows, out, lse_out, (hipStream_t) stream),
+                  "coattn launch") ? 0 : -1;
 }
 
 extern "C" int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream) {

@@ -39,6 +39,8 @@ struct MergeArgs {
     const float2 * pml;
     float * O, * m, * l;            // [nkv][rows][hd], [nkv][rows]
     uint32_t n_slots, nkv, qr, rows;
+    uint16_t * Oh = nullptr;        // non-null: write the reply format instead of (O, m, l): Oh = f16(O / l) [nkv][rows][hd]
+    float * lse = nullptr;          // and lse = m + log l [nkv][rows] (0 and -inf where l = 0)
 };
 
 hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st);
@@ -48,6 +50,12 @@ hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t
 hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
                       hipEvent_t ev1 = nullptr);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
+hipError_t launch_merge_partial(int hd, float * O, float * m, float * l, const float * O2, const float * m2, const float * l2,
+                                uint64_t rows, hipStream_t st);
+hipError_t launch_normalise(int hd, const float * O, const float * m, const float * l, uint64_t rows, uint16_t * Oh,
+                            float * lse, hipStream_t st);
+hipError_t launch_coattn(int hd, const uint16_t * Oh, const float * lse, const float * Oloc, const float * mloc,
+                         const float * lloc, uint64_t rows, float * out, float * lse_out, hipStream_t st);
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb);
 int decode_variant();
 

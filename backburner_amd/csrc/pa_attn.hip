@@ -318,7 +318,7 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
             } else {
                 const float mul = a.qmode == 0 ? 1.0f : a.scale;
                 #pragma unroll
-                for (int j = 0; j < 8; j++) { qh[rt][kd][j] = (_Float16) (x[j] * mul); ql[rt][kd][j] = (_Float16) 0.0f; }
+                for (int j = 0; j < 8; j++) { qh[rt][kd][j] = (_Float16) pa_f32(x[j] * mul); ql[rt][kd][j] = (_Float16) 0.0f; }
             }
         }
     }
@@ -512,6 +512,22 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
 }
 
 // ---------------------------------------------------------------- split-K fold as its own kernel
+// The reply format of a merged row (the ATTN reply, phone-attn.h:651-655), written in place of (O, m, l) when the call
+// asks for it: Oh = f16(O * (1 / L)) (0 where L = 0) for k consecutive dims, lse = M ln 2 + log L by the thread given
+// `row_stats`. The same roundings as storing (O, m, l) and normalising them afterwards.
+template <int K>
+__device__ __forceinline__ void merge_write_reply(const MergeArgs & a, size_t off, const float * o, float M, float L, uint32_t r,
+                                                  bool row_stats) {
+    #pragma clang fp contract(off)
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    #pragma unroll
+    for (int k = 0; k < K; k++) a.Oh[off + k] = __builtin_bit_cast(uint16_t, (_Float16) pa_f32(o[k] * inv));
+    if (row_stats) {
+        const float mm = M == -INFINITY ? -INFINITY : M * PA_LN2;
+        a.lse[r] = L > 0.0f ? mm + logf(L) : -INFINITY;
+    }
+}
+
 // Used when one call needs several attention launches (more than MAXP pages). One workgroup per output row; thread t
 // folds dims 4*(t % (HD/4)) over slots t / (HD/4), t / (HD/4) + SG, ...
 template <int HD>
@@ -547,7 +563,13 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     if (d4 == 0) redl[sg] = L;
     __syncthreads();
     if (sg == 0) {
-        for (int q = 1; q < SG; q++) { acc += red[q][d4]; if (d4 == 0) L += redl[q]; }
+        for (int q = 1; q < SG; q++) acc += red[q][d4];
+        for (int q = 1; q < SG; q++) L += redl[q];                    // every thread: the reply needs L
+        if (a.Oh) {
+            const float ov[4] = {acc[0], acc[1], acc[2], acc[3]};
+            merge_write_reply<4>(a, (size_t) r * HD + 4 * d4, ov, M, L, r, d4 == 0);
+            return;
+        }
         *(pa_f4 *) (a.O + (size_t) r * HD + 4 * d4) = acc;
         if (d4 == 0) { a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[r] = L; }
     }
@@ -607,6 +629,10 @@ __global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
         float acc = 0.0f;
         #pragma unroll
         for (int seg = 0; seg < 8; seg++) acc += sP[seg][t];
+        if (a.Oh) {
+            merge_write_reply<1>(a, (size_t) r * HD + 32 * dq + t, &acc, M, sL[0] + sL[1] + sL[2] + sL[3], r, dq == 0 && t == 0);
+            return;
+        }
         a.O[(size_t) r * HD + 32 * dq + t] = acc;
         if (dq == 0 && t == 0) {
             a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2;
@@ -649,6 +675,11 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const MergeArgs a) {
         const float w = __builtin_amdgcn_exp2f(ml[s].x - Ms);       // -inf (an empty or absent slot) -> 0
         acc += w * o[s];
         L += w * ml[s].y;
+    }
+    if (a.Oh) {
+        const float ov[4] = {acc[0], acc[1], acc[2], acc[3]};
+        merge_write_reply<4>(a, (size_t) r * HD + 4 * d4, ov, M, L, r, d4 == 0);
+        return;
     }
     *(pa_f4 *) (a.O + (size_t) r * HD + 4 * d4) = acc;
     if (d4 == 0) { a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[r] = L; }

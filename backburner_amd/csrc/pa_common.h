@@ -40,6 +40,11 @@ __device__ __forceinline__ uint32_t pa_pair_byte(uint32_t x1, uint32_t x0, int e
 
 __device__ __forceinline__ float pa_f16_bits_to_f32(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 
+// x as an opaque fp32 value in a register. A conversion to fp16 of a product would otherwise become v_fma_mix*_f16,
+// which rounds the exact product to fp16 once; the reference rounds to fp32 first and then to fp16 (f2h(a * b)), and
+// the two differ where the fp32 product sits on an fp16 rounding midpoint.
+__device__ __forceinline__ float pa_f32(float x) { asm("" : "+v"(x)); return x; }
+
 // Unaligned loads from a byte pointer (gfx9+ vector memory accepts byte-aligned dword addresses).
 template <typename T> __device__ __forceinline__ T pa_ld(const uint8_t * p) { T v; __builtin_memcpy(&v, p, sizeof(T)); return v; }
 

@@ -239,7 +239,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             for (int kk = 0; kk < 8; kk++) {
                 mm_h8 f;
                 #pragma unroll
-                for (int t = 0; t < 8; t++) f[t] = (_Float16) (x[2 * kk + t / 4][t % 4] * qs);
+                for (int t = 0; t < 8; t++) f[t] = (_Float16) pa_f32(x[2 * kk + t / 4][t % 4] * qs);   // f2h(q * scale)
                 Qf[kk] = f;
             }
         }

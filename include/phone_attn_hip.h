@@ -115,6 +115,31 @@ int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, int64_t voca
  * that kernel alone with hipEventElapsedTime. One call consumes the pair. Returns 0. */
 int pa_hip_ws_time_next(pa_hip_ws * ws, void * ev_start, void * ev_end);
 
+/* ---------------------------------------------------------------- 3. the reply side (device epilogues) */
+/* The ATTN reply of one call in one step: the partial attention of pa_hip_attn, returned in the reply format of
+ * phone-attn.h:651-655 - Oh = f16(O / l) (fp16 bits, [nkv][rows][hd]; 0 where l = 0) and lse = m + log l (fp32
+ * [nkv][rows]; -inf where l = 0). When the call is split over several workgroups the split-K merge writes this format
+ * itself (no fp32 O round trip); a single-chunk call is normalised by one more kernel. Oh must be 8-byte aligned.
+ * Returns 0 once enqueued, -1 on a bad argument. */
+int pa_hip_attn_reply(pa_hip_ws * ws, const pa_hip_shape * shape, const void * const * k_pages, const void * const * v_pages,
+                      const uint32_t * nkeys, int n_pages, const float * Q, uint16_t * Oh, float * lse, void * stream);
+/* pa::merge_partial (phone-attn.h:231-239) on the device: fold the partial (O2, m2, l2) into (O, m, l) in place, `rows`
+ * rows of hd (128 or 256) floats, m in natural-log units. A row with l2 <= 0 is left as it is; a row with l <= 0 takes
+ * the second partial; otherwise M = max(m, m2), O = O e^(m-M) + O2 e^(m2-M), l = l e^(m-M) + l2 e^(m2-M), m = M (the
+ * server's merge of the partials of several engines). O and O2 16-byte aligned. Returns 0 or -1. */
+int pa_hip_merge_partial(float * O, float * m, float * l, const float * O2, const float * m2, const float * l2,
+                         uint64_t rows, uint32_t hd, void * stream);
+/* The reply format (phone-attn.h:651-655) of a partial: Oh = f16(O * (1 / l)) (0 where l <= 0), lse = m + log l (-inf
+ * where l <= 0). O 16-byte, Oh 8-byte aligned. Returns 0 or -1. */
+int pa_hip_normalise(const float * O, const float * m, const float * l, uint64_t rows, uint32_t hd, uint16_t * Oh,
+                     float * lse, void * stream);
+/* The receiver's co-attention merge: a reply (Oh, lse) enters the receiver's attention as the partial O_unnorm = Oh,
+ * S = 1, M = lse (phone-attn.h:21); it is merged with the receiver's own partial over its recent keys (O_loc, m_loc,
+ * l_loc) as pa::merge_partial does, and normalised: out = the attention over both key sets (fp32 [rows][hd]; 0 where
+ * neither side has keys), lse_out (optional, may be NULL) = its log-sum-exp. Oh 8-byte, O_loc and out 16-byte aligned.
+ * No code in the reference tree (the receiver is the fork's Metal flash attention). Returns 0 or -1. */
+int pa_hip_coattn_merge(const uint16_t * Oh, const float * lse, const float * O_loc, const float * m_loc, const float * l_loc,
+                        uint64_t rows, uint32_t hd, float * out, float * lse_out, void * stream);
 /* q8_0 / q4_0 quantizer of the library (ggml quantize_row_q8_0_ref / q4_0_ref semantics; the q8_0 one prepares Q in
  * PA_QMODE_GGML): n fp32 values (multiple of 32) at x -> blocks at y, both device pointers. Returns 0 or -1. */
 int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream);

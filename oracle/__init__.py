@@ -51,6 +51,7 @@ def lib() -> C.CDLL:
     L.orc_attn_ggml.argtypes = [C.POINTER(Shape), vp, vp, vp, i64, vp, vp, vp, C.c_int]
     L.orc_merge_partial.argtypes = [vp, vp, vp, vp, vp, vp, i64, C.c_int]
     L.orc_normalise.argtypes = [vp, vp, vp, i64, C.c_int, vp, vp]
+    L.orc_coattn_merge.argtypes = [vp, vp, vp, vp, vp, i64, C.c_int, vp, vp]
     L.orc_accept.argtypes = [vp, C.c_int, i64, vp, vp, vp, vp]
     L.orc_quantize_q_row.argtypes = [vp, C.c_int, vp]
     _lib = L
@@ -155,11 +156,25 @@ def merge_partial(O, m, l, O2, m2, l2):
 
 
 def normalise(O, m, l):
+    O = np.ascontiguousarray(O, np.float32)
+    m = np.ascontiguousarray(m, np.float32); l = np.ascontiguousarray(l, np.float32)
     rows, hd = O.shape
     Oh = np.empty((rows, hd), np.uint16)
     lse = np.empty(rows, np.float32)
     lib().orc_normalise(_p(O), _p(m), _p(l), rows, hd, _p(Oh), _p(lse))
     return Oh, lse
+
+
+def coattn_merge(Oh, lse, O_loc, m_loc, l_loc):
+    """The receiver's merge of a reply (Oh fp16 bits, lse) with its partial (O_loc, m_loc, l_loc): (out, lse_out)."""
+    rows, hd = O_loc.shape
+    Oh = np.ascontiguousarray(Oh, np.uint16); lse = np.ascontiguousarray(lse, np.float32)
+    O_loc = np.ascontiguousarray(O_loc, np.float32)
+    m_loc = np.ascontiguousarray(m_loc, np.float32); l_loc = np.ascontiguousarray(l_loc, np.float32)
+    out = np.empty((rows, hd), np.float32)
+    lse_out = np.empty(rows, np.float32)
+    lib().orc_coattn_merge(_p(Oh), _p(lse), _p(O_loc), _p(m_loc), _p(l_loc), rows, hd, _p(out), _p(lse_out))
+    return out, lse_out
 
 
 def accept(logits: np.ndarray, draft: np.ndarray):

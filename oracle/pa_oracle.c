@@ -402,6 +402,27 @@ void orc_normalise(const float * O, const float * m, const float * l, int64_t ro
     }
 }
 
+/* The receiver's co-attention slot (phone-attn.h:21): the reply (Oh, lse) enters as the partial O_unnorm = Oh, S = 1,
+ * M = lse; it is folded into the receiver's partial by orc_merge_partial (phone-attn.h:231-239) and the result is
+ * normalised as O * (1 / l) (phone-attn.h:651-652), lse_out = m + log l. A composition of the two reference formulas;
+ * the receiver's own kernel is in the un-vendored fork. */
+void orc_coattn_merge(const uint16_t * Oh, const float * lse, const float * Oloc, const float * mloc, const float * lloc,
+                      int64_t rows, int hd, float * out, float * lse_out) {
+    float * O2 = (float *) malloc(sizeof(float) * (size_t) hd);
+    for (int64_t r = 0; r < rows; r++) {
+        float m = mloc[r], l = lloc[r];
+        const float one = 1.0f;
+        float * o = out + r * hd;
+        memcpy(o, Oloc + r * hd, sizeof(float) * (size_t) hd);
+        for (int d = 0; d < hd; d++) O2[d] = orc_f16_to_f32(Oh[r * hd + d]);
+        orc_merge_partial(o, &m, &l, O2, &lse[r], &one, 1, hd);
+        const float inv = l > 0 ? 1.0f / l : 0.0f;
+        for (int d = 0; d < hd; d++) o[d] = o[d] * inv;
+        if (lse_out) lse_out[r] = l > 0 ? m + logf(l) : -INFINITY;
+    }
+    free(O2);
+}
+
 void orc_accept(const float * logits, int n_rows, int64_t vocab, const int32_t * draft, int32_t * argmax,
                 int32_t * k, int32_t * bonus) {
     for (int i = 0; i < n_rows; i++) {

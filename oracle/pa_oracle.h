@@ -90,6 +90,10 @@ void orc_merge_partial(float * O, float * m, float * l, const float * O2, const 
                        int64_t rows, int hd);
 /* reply normalisation (phone-attn.h:651-655): Oh = f16(O/l) (0 if l <= 0), lse = m + log(l) (-inf if l <= 0) */
 void orc_normalise(const float * O, const float * m, const float * l, int64_t rows, int hd, uint16_t * Oh, float * lse);
+/* the receiver's co-attention merge of a reply (Oh, lse) with its own partial, normalised (phone-attn.h:21, 231-239,
+ * 651-655); lse_out may be NULL */
+void orc_coattn_merge(const uint16_t * Oh, const float * lse, const float * Oloc, const float * mloc, const float * lloc,
+                      int64_t rows, int hd, float * out, float * lse_out);
 
 /* greedy acceptance over logits [n_rows][vocab] fp32 and a draft of n_rows-1 tokens: argmax[i] (lowest index on ties;
  * the first NaN wins, as numpy.argmax), k = length of the longest prefix with argmax[i] == draft[i], bonus = argmax[k]. */
