@@ -98,6 +98,12 @@ def lib() -> C.CDLL:
     L.pa_hip_merge_partial.argtypes = [vp, vp, vp, vp, vp, vp, C.c_uint64, C.c_uint32, vp]
     L.pa_hip_normalise.restype = C.c_int
     L.pa_hip_normalise.argtypes = [vp, vp, vp, C.c_uint64, C.c_uint32, vp, vp, vp]
+    L.pa_hip_append_rows.restype = C.c_int
+    L.pa_hip_append_rows.argtypes = [C.POINTER(Shape), C.POINTER(vp), C.POINTER(vp), C.c_int, C.c_uint32, C.c_uint32, vp, vp,
+                                     C.c_uint32, C.c_int, vp]
+    L.pa_hip_append_f32.restype = C.c_int
+    L.pa_hip_append_f32.argtypes = [C.POINTER(Shape), C.POINTER(vp), C.POINTER(vp), C.c_int, C.c_uint32, C.c_uint32, vp, vp,
+                                    C.c_uint32, vp]
     L.pa_hip_coattn_merge.restype = C.c_int
     L.pa_hip_coattn_merge.argtypes = [vp, vp, vp, vp, vp, C.c_uint64, C.c_uint32, vp, vp, vp]
     _hip = L
@@ -321,6 +327,31 @@ def normalise_device(O: int, m: int, l: int, rows: int, hd: int, Oh: int, lse: i
 def coattn_merge_device(Oh: int, lse: int, O_loc: int, m_loc: int, l_loc: int, rows: int, hd: int, out: int, lse_out=None,
                         stream=None) -> None:
     _check(lib().pa_hip_coattn_merge(Oh, lse, O_loc, m_loc, l_loc, rows, hd, out, lse_out, stream), "pa_hip_coattn_merge")
+
+
+def append_rows(shape: Shape, pages: Pages, page_keys: int, pos0: int, K: int, V: int, n: int, store_f16: bool = False,
+                stream=None) -> None:
+    """pa_hip_append_rows: n received rows (device or host pointers K, V) into the layer's pages at pos0."""
+    m = max(len(pages.k), 1)
+    kp = (C.c_void_p * m)(*pages.k); vp = (C.c_void_p * m)(*pages.v)
+    _check(lib().pa_hip_append_rows(C.byref(shape), kp, vp, len(pages.k), page_keys, pos0, K, V, n, int(store_f16), stream),
+           "pa_hip_append_rows")
+
+
+def append_f32(shape: Shape, pages: Pages, page_keys: int, pos0: int, K: int, V: int, n: int, stream=None) -> None:
+    """pa_hip_append_f32: fp32 K/V [n][nkv][hd] (device pointers) quantized into the pages at pos0."""
+    m = max(len(pages.k), 1)
+    kp = (C.c_void_p * m)(*pages.k); vp = (C.c_void_p * m)(*pages.v)
+    _check(lib().pa_hip_append_f32(C.byref(shape), kp, vp, len(pages.k), page_keys, pos0, K, V, n, stream), "pa_hip_append_f32")
+
+
+def alloc_pages(n_pages: int, page_bytes: int) -> Pages:
+    """n_pages device pages of page_bytes each for K and for V (contents undefined), as engine::alloc_page does."""
+    ks, vs, bufs = [], [], []
+    for _ in range(n_pages):
+        kb = DeviceBuffer(page_bytes); vb = DeviceBuffer(page_bytes)
+        ks.append(kb.ptr); vs.append(vb.ptr); bufs += [kb, vb]
+    return Pages(ks, vs, [0] * n_pages, bufs)
 
 
 def make_shape(nkv: int, rows: int, hd: int, fmt: int, qmode: int = QMODE_GGML, scale: float | None = None,

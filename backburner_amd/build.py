@@ -32,7 +32,8 @@ HIP_FLAGS = [
 SRC_FLAGS = {"pa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 LIBS = {
-    "libpa_hip.so": ["pa_attn.hip", "pa_decode.hip", "pa_mma.hip", "pa_accept.hip", "pa_reply.hip", "pa_abi.cpp"],
+    "libpa_hip.so": ["pa_attn.hip", "pa_decode.hip", "pa_mma.hip", "pa_accept.hip", "pa_reply.hip", "pa_ingest.hip",
+                     "pa_abi.cpp"],
     "libpa_synth.so": ["pa_synth.hip"],
 }
 

@@ -538,6 +538,81 @@ extern "C" int pa_hip_coattn_merge(const uint16_t * Oh, const float * lse, const
                   "coattn launch") ? 0 : -1;
 }
 
+// ---------------------------------------------------------------- 4. KV ingest into HBM pages
+namespace {
+// shared checks and the page-segment walk of an APPEND: positions pos0 .. pos0+n-1 over pages of page_keys keys
+bool append_ok(const char * fn, const pa_hip_shape * s, void * const * kp, void * const * vp, int n_pages, uint32_t page_keys,
+               uint32_t pos0, uint32_t n) {
+    const std::string f(fn);
+    if (!s) { set_err(f + ": null shape"); return false; }
+    if (s->hd != 128 && s->hd != 256) { set_err(f + ": hd must be 128 or 256"); return false; }
+    if (s->fmt > PA_FMT_Q4_0 || s->nkv == 0) { set_err(f + ": bad fmt or nkv"); return false; }
+    const uint32_t hbmin = head_bytes((int) s->fmt, (int) s->hd);
+    if (s->hb < hbmin || (uint64_t) s->rs < (uint64_t) s->nkv * s->hb) { set_err(f + ": hb / rs too small"); return false; }
+    if (page_keys == 0) { set_err(f + ": page_keys must be > 0"); return false; }
+    if (n == 0) return true;
+    if ((uint64_t) pos0 + n > (uint64_t) n_pages * page_keys) { set_err(f + ": positions past the last page"); return false; }
+    if (!kp || !vp) { set_err(f + ": null page table"); return false; }
+    for (uint64_t pi = pos0 / page_keys; pi <= (pos0 + (uint64_t) n - 1) / page_keys; pi++)
+        if (!kp[pi] || !vp[pi]) { set_err(f + ": null page " + std::to_string(pi)); return false; }
+    if (2ull * std::min(n, page_keys) * s->nkv * (s->hd / 32) >= (1ull << 31)) { set_err(f + ": segment too large"); return false; }
+    return true;
+}
+}  // namespace
+
+extern "C" int pa_hip_append_rows(const pa_hip_shape * s, void * const * k_pages, void * const * v_pages, int n_pages,
+                                  uint32_t page_keys, uint32_t pos0, const void * K, const void * V, uint32_t n, int store_f16,
+                                  void * stream) {
+    const bool f16 = store_f16 && s && s->fmt == PA_FMT_Q8_0;      // store_rows converts q8_0 only (phone-attn.h:305)
+    const uint32_t srs = s ? (f16 ? s->nkv * s->hd * 2 : s->rs) : 0;
+    if (!append_ok("pa_hip_append_rows", s, k_pages, v_pages, n_pages, page_keys, pos0, n)) return -1;
+    if (n > 0 && (!K || !V)) { set_err("pa_hip_append_rows: null K/V"); return -1; }
+    hipStream_t st = (hipStream_t) stream;
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t pos = pos0 + done, pi = pos / page_keys, off = pos % page_keys;
+        const uint32_t take = std::min(n - done, page_keys - off);
+        uint8_t * kd = (uint8_t *) k_pages[pi] + (size_t) off * srs;
+        uint8_t * vd = (uint8_t *) v_pages[pi] + (size_t) off * srs;
+        const uint8_t * ks = (const uint8_t *) K + (size_t) done * s->rs;
+        const uint8_t * vs = (const uint8_t *) V + (size_t) done * s->rs;
+        if (!f16) {                                                   // rows as received: one copy per page segment
+            if (!hip_ok(hipMemcpyAsync(kd, ks, (size_t) take * s->rs, hipMemcpyDefault, st), "hipMemcpyAsync K") ||
+                !hip_ok(hipMemcpyAsync(vd, vs, (size_t) take * s->rs, hipMemcpyDefault, st), "hipMemcpyAsync V"))
+                return -1;
+        } else {
+            AppendArgs a;
+            a.kdst = kd; a.vdst = vd; a.ksrc = ks; a.vsrc = vs;
+            a.n = take; a.nkv = s->nkv; a.hd = s->hd; a.rs = srs; a.hb = s->hd * 2; a.src_rs = s->rs; a.src_hb = s->hb;
+            a.fmt = PA_FMT_F16;
+            if (!hip_ok(launch_append(false, a, st), "append f16 launch")) return -1;
+        }
+        done += take;
+    }
+    return 0;
+}
+
+extern "C" int pa_hip_append_f32(const pa_hip_shape * s, void * const * k_pages, void * const * v_pages, int n_pages,
+                                 uint32_t page_keys, uint32_t pos0, const float * K, const float * V, uint32_t n, void * stream) {
+    if (!append_ok("pa_hip_append_f32", s, k_pages, v_pages, n_pages, page_keys, pos0, n)) return -1;
+    if (n > 0 && (!K || !V)) { set_err("pa_hip_append_f32: null K/V"); return -1; }
+    if (((uintptr_t) K & 3) || ((uintptr_t) V & 3)) { set_err("pa_hip_append_f32: K/V must be 4-byte aligned"); return -1; }
+    hipStream_t st = (hipStream_t) stream;
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t pos = pos0 + done, pi = pos / page_keys, off = pos % page_keys;
+        const uint32_t take = std::min(n - done, page_keys - off);
+        AppendArgs a;
+        a.kdst = (uint8_t *) k_pages[pi] + (size_t) off * s->rs;
+        a.vdst = (uint8_t *) v_pages[pi] + (size_t) off * s->rs;
+        a.ksrc = K + (size_t) done * s->nkv * s->hd;
+        a.vsrc = V + (size_t) done * s->nkv * s->hd;
+        a.n = take; a.nkv = s->nkv; a.hd = s->hd; a.rs = s->rs; a.hb = s->hb; a.src_rs = 0; a.src_hb = 0;
+        a.fmt = (int) s->fmt;
+        if (!hip_ok(launch_append(true, a, st), "append quantize launch")) return -1;
+        done += take;
+    }
+    return 0;
+}
+
 extern "C" int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream) {
     if (fmt != PA_FMT_Q8_0 && fmt != PA_FMT_Q4_0) { set_err("pa_hip_quantize: fmt must be 1 or 2"); return -1; }
     if (n < 0 || n % 32 || (n > 0 && (!x || !y))) { set_err("pa_hip_quantize: n must be a multiple of 32"); return -1; }

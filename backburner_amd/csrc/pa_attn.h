@@ -50,6 +50,16 @@ hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t
 hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
                       hipEvent_t ev1 = nullptr);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
+
+struct AppendArgs {                 // one page segment of an APPEND: rows j = 0 .. n-1
+    uint8_t * kdst, * vdst;         // the segment's first row in the K / V page
+    const void * ksrc, * vsrc;      // fp32 [n][nkv][hd] (append_quant_kernel) or received rows (append_f16_kernel)
+    uint32_t n, nkv, hd;
+    uint32_t rs, hb;                // stored row and head strides (bytes)
+    uint32_t src_rs, src_hb;        // received row and head strides (append_f16_kernel)
+    int fmt;                        // stored format (append_quant_kernel)
+};
+hipError_t launch_append(bool from_f32, const AppendArgs & a, hipStream_t st);
 hipError_t launch_merge_partial(int hd, float * O, float * m, float * l, const float * O2, const float * m2, const float * l2,
                                 uint64_t rows, hipStream_t st);
 hipError_t launch_normalise(int hd, const float * O, const float * m, const float * l, uint64_t rows, uint16_t * Oh,

@@ -685,43 +685,6 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const MergeArgs a) {
     if (d4 == 0) { a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[r] = L; }
 }
 
-// ---------------------------------------------------------------- device quantizers
-// ggml quantize_row_q8_0_ref / quantize_row_q4_0_ref, one thread per 32-block. Every float expression rounds as written
-// (no FMA contraction), as the oracle's C restatement does.
-__global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, uint8_t * __restrict__ y, int64_t nblk, int fmt) {
-    #pragma clang fp contract(off)
-    const int64_t b = (int64_t) blockIdx.x * 256 + threadIdx.x;
-    if (b >= nblk) return;
-    const float * xb = x + b * 32;
-    if (fmt == 1) {
-        uint8_t * o = y + b * 34;
-        float amax = 0.0f;
-        for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(xb[j]));
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        const uint16_t dh = __builtin_bit_cast(uint16_t, (_Float16) d);
-        o[0] = (uint8_t) (dh & 0xff); o[1] = (uint8_t) (dh >> 8);
-        for (int j = 0; j < 32; j++) o[2 + j] = (uint8_t) (int8_t) roundf(xb[j] * id);
-    } else {
-        uint8_t * o = y + b * 18;
-        float amax = 0.0f, mx = 0.0f;
-        for (int j = 0; j < 32; j++) { const float v = xb[j]; if (amax < fabsf(v)) { amax = fabsf(v); mx = v; } }
-        const float d = mx / -8.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        // d = 0 / -8 is -0 (fp16 0x8000); keep the sign bit explicitly (a fused f32->f16 multiply-add would drop it)
-        const uint16_t dh = d == 0.0f ? (uint16_t) ((__builtin_bit_cast(uint32_t, mx) >> 16) & 0x8000u) ^ 0x8000u
-                                      : __builtin_bit_cast(uint16_t, (_Float16) d);
-        o[0] = (uint8_t) (dh & 0xff); o[1] = (uint8_t) (dh >> 8);
-        for (int j = 0; j < 16; j++) {
-            const float x0 = xb[j] * id, x1 = xb[16 + j] * id;
-            int q0 = (int8_t) (x0 + 8.5f), q1 = (int8_t) (x1 + 8.5f);
-            q0 = q0 > 15 ? 15 : q0;
-            q1 = q1 > 15 ? 15 : q1;
-            o[2 + j] = (uint8_t) (q0 | (q1 << 4));
-        }
-    }
-}
-
 // ---------------------------------------------------------------- launch table
 template <int HD, int FMT, int RT, int WR, int WK, int NB>
 static hipError_t launch_attn(const AttnArgs & a, uint32_t grid, hipStream_t st) {
@@ -795,13 +758,6 @@ hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
     if (hd == 128) hipLaunchKernelGGL(merge_kernel<128>, dim3(grid), dim3(256), 0, st, a);
     else if (hd == 256) hipLaunchKernelGGL(merge_kernel<256>, dim3(grid), dim3(256), 0, st, a);
     else return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-
-hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st) {
-    const int64_t nblk = n / 32;
-    if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL(quantize_kernel, dim3((uint32_t) ((nblk + 255) / 256)), dim3(256), 0, st, x, (uint8_t *) y, nblk, fmt);
     return hipGetLastError();
 }
 

@@ -52,6 +52,7 @@ def lib() -> C.CDLL:
     L.orc_merge_partial.argtypes = [vp, vp, vp, vp, vp, vp, i64, C.c_int]
     L.orc_normalise.argtypes = [vp, vp, vp, i64, C.c_int, vp, vp]
     L.orc_coattn_merge.argtypes = [vp, vp, vp, vp, vp, i64, C.c_int, vp, vp]
+    L.orc_store_rows_f16.argtypes = [vp, i64, C.c_int, C.c_int, C.c_uint32, C.c_uint32, vp]
     L.orc_accept.argtypes = [vp, C.c_int, i64, vp, vp, vp, vp]
     L.orc_quantize_q_row.argtypes = [vp, C.c_int, vp]
     _lib = L
@@ -163,6 +164,25 @@ def normalise(O, m, l):
     lse = np.empty(rows, np.float32)
     lib().orc_normalise(_p(O), _p(m), _p(l), rows, hd, _p(Oh), _p(lse))
     return Oh, lse
+
+
+def store_rows_f16(rows: np.ndarray, n: int, nkv: int, hd: int, rs: int, hb: int) -> np.ndarray:
+    """store_rows' q8_0 -> f16 conversion (phone-attn.h:305-319): the stored rows as fp16 bits [n][nkv*hd]."""
+    rows = np.ascontiguousarray(rows, np.uint8)
+    out = np.empty((n, nkv * hd), np.uint16)
+    lib().orc_store_rows_f16(_p(rows), n, nkv, hd, rs, hb, _p(out))
+    return out
+
+
+def rows_from_f32(fmt: int, X: np.ndarray, rs: int, hb: int) -> np.ndarray:
+    """fp32 [n][nkv][hd] -> the row bytes [n*rs] of that format (each head's hd values quantized as one row, padding 0)."""
+    n, nkv, hd = X.shape
+    out = np.zeros((n, rs), np.uint8)
+    for h in range(nkv):
+        q = quantize(fmt, np.ascontiguousarray(X[:, h, :]).reshape(-1)) if fmt != F16 else \
+            f32_to_f16(X[:, h, :].reshape(-1)).view(np.uint8)
+        out[:, h * hb:h * hb + head_bytes(fmt, hd)] = q.reshape(n, -1)
+    return out.reshape(-1)
 
 
 def coattn_merge(Oh, lse, O_loc, m_loc, l_loc):

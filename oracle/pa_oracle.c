@@ -402,6 +402,19 @@ void orc_normalise(const float * O, const float * m, const float * l, int64_t ro
     }
 }
 
+/* store_rows with store_f16 (phone-attn.h:305-319): n received q8_0 rows (row stride rs, head stride hb) stored as f16
+ * rows [n][nkv][hd], element f16(d * q) */
+void orc_store_rows_f16(const uint8_t * src, int64_t n, int nkv, int hd, uint32_t rs, uint32_t hb, uint16_t * dst) {
+    for (int64_t j = 0; j < n; j++)
+        for (int h = 0; h < nkv; h++)
+            for (int b = 0; b < hd / 32; b++) {
+                const uint8_t * blk = src + (size_t) j * rs + (size_t) h * hb + (size_t) b * 34;
+                const float d = rd_f16(blk);
+                for (int i = 0; i < 32; i++)
+                    dst[((size_t) j * nkv + h) * hd + b * 32 + i] = orc_f32_to_f16(d * (float) (int8_t) blk[2 + i]);
+            }
+}
+
 /* The receiver's co-attention slot (phone-attn.h:21): the reply (Oh, lse) enters as the partial O_unnorm = Oh, S = 1,
  * M = lse; it is folded into the receiver's partial by orc_merge_partial (phone-attn.h:231-239) and the result is
  * normalised as O * (1 / l) (phone-attn.h:651-652), lse_out = m + log l. A composition of the two reference formulas;

@@ -90,6 +90,8 @@ void orc_merge_partial(float * O, float * m, float * l, const float * O2, const 
                        int64_t rows, int hd);
 /* reply normalisation (phone-attn.h:651-655): Oh = f16(O/l) (0 if l <= 0), lse = m + log(l) (-inf if l <= 0) */
 void orc_normalise(const float * O, const float * m, const float * l, int64_t rows, int hd, uint16_t * Oh, float * lse);
+/* store_rows' q8_0 -> f16 conversion (phone-attn.h:305-319): rows [n] of stride rs -> f16 [n][nkv][hd] */
+void orc_store_rows_f16(const uint8_t * src, int64_t n, int nkv, int hd, uint32_t rs, uint32_t hb, uint16_t * dst);
 /* the receiver's co-attention merge of a reply (Oh, lse) with its own partial, normalised (phone-attn.h:21, 231-239,
  * 651-655); lse_out may be NULL */
 void orc_coattn_merge(const uint16_t * Oh, const float * lse, const float * Oloc, const float * mloc, const float * lloc,
