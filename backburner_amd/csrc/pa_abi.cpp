@@ -268,9 +268,9 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
 // many rows per KV head (verify, prefill; head dim 128): mma_kernel over row blocks of 32*NW rows x chunks of tiles
 int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
              const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
-    const uint32_t tile = 32;
     const int nw_env = env_int("PA_HIP_MMA_NW", 0);
     const uint32_t nw = nw_env == 2 || nw_env == 4 || nw_env == 8 ? (uint32_t) nw_env : s->rows > 128 ? 8u : s->rows > 64 ? 4u : 2u;
+    const uint32_t tile = 32;
     const uint32_t nrb = (s->rows + 32 * nw - 1) / (32 * nw), qr = nrb * 32 * nw;
     const uint32_t units = s->nkv * nrb;
     // key chunks: about PA_HIP_MMA_TARGET workgroups in all (resident ones: 1 of 8 waves, 2 of 4, 4 of 2 per CU)

@@ -115,6 +115,107 @@ __device__ __forceinline__ float mm_sum32(float v) {    // sum over lanes l and 
     return __builtin_bit_cast(float, (unsigned) t[0]) + __builtin_bit_cast(float, (unsigned) t[1]);
 }
 
+// Page cursor (scalar): the page holding a tile, its tile range and key count. A cursor moves only when a tile leaves
+// its page, so the common case reads no kernel argument memory (whose scalar loads would also wait for the LDS
+// operations in flight).
+struct MmCursor {
+    uint32_t pg, tb, te, nk;
+    const uint8_t * kb, * vb;
+    __device__ __forceinline__ void init(const AttnArgs & a) {
+        pg = 0; tb = a.cstart[0]; te = a.cstart[1]; nk = a.pstart[1] - a.pstart[0]; kb = a.kp[0]; vb = a.vp[0];
+    }
+    __device__ __forceinline__ void seek(const AttnArgs & a, uint32_t tau) {
+        while (tau >= te) {
+            pg++;
+            tb = te;
+            te = a.cstart[pg + 1];
+            nk = a.pstart[pg + 1] - a.pstart[pg];
+            kb = a.kp[pg];
+            vb = a.vp[pg];
+            __builtin_amdgcn_s_waitcnt(0xc07f);                      // lgkmcnt(0): no scalar load left outstanding
+        }
+    }
+};
+
+// The query rows as the B operand (lane (h2, n) holds row n, dims 16kk + 8h2 + t): PRE -> ggml's q8_0 per 32-block in
+// base-2 units, else f16(q * scale) (or f16(q) for f16 K in PA_QMODE_GGML, ggml's f16 vec_dot type)
+template <int FMT, bool PRE>
+__device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32_t row, bool rlive, int h2, mm_h8 (&Qf)[8]) {
+    const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * MM_HD + 8 * h2;
+    const uint32_t qmask = rlive ? 0xffffffffu : 0u;
+    pa_f4 x[16];
+    #pragma unroll
+    for (int kk = 0; kk < 8; kk++) {
+        x[2 * kk] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 16 * kk)) & qmask);
+        x[2 * kk + 1] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 16 * kk + 4)) & qmask);
+    }
+    const float scale = a.scale;
+    if constexpr (PRE) {
+        // ggml q8_0 per 32-block b = k-steps 2b, 2b+1: this lane holds 16 of its values, lane ^ 32 the other 16
+        #pragma clang fp contract(off)
+        #pragma unroll
+        for (int b = 0; b < 4; b++) {
+            float am = 0.0f;
+            #pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const pa_f4 v = x[4 * b + j];
+                am = fmaxf(am, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+            }
+            am = mm_max32(am);
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const float dq = (float) (_Float16) d * (scale * MM_LOG2E);   // the fp16 block scale (as ggml stores it)
+                                                                          // * scale, in base-2 units
+            #pragma unroll
+            for (int kq = 0; kq < 2; kq++) {
+                mm_h8 f;
+                #pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const float xv = x[4 * b + 2 * kq + t / 4][t % 4];
+                    f[t] = (_Float16) (roundf(xv * id) * dq);
+                }
+                Qf[2 * b + kq] = f;
+            }
+        }
+    } else {
+        const float qs = a.qmode == 0 ? 1.0f : scale;
+        #pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            mm_h8 f;
+            #pragma unroll
+            for (int t = 0; t < 8; t++) f[t] = (_Float16) pa_f32(x[2 * kk + t / 4][t % 4] * qs);   // f2h(q * scale)
+            Qf[kk] = f;
+        }
+    }
+}
+
+// Row n's result: the sum over both lanes, O rebased from the reference max to the exact one; the final (O, m, l)
+// for a single-chunk call, else split-K slot c
+__device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&O)[4], float mref, float mx, float lsum,
+                                             uint32_t h, uint32_t row, bool rlive, int h2, uint32_t c) {
+    const float lt = mm_sum32(lsum);
+    const float f = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mx);
+    if (!rlive) return;
+    const bool direct = a.n_chunks == 1 && a.fused;
+    float * dst = direct ? a.O + ((size_t) h * a.rows + row) * MM_HD
+                         : a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row) * MM_HD;
+    #pragma unroll
+    for (int db = 0; db < 4; db++)
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const pa_f4 v = {O[db][4 * j] * f, O[db][4 * j + 1] * f, O[db][4 * j + 2] * f, O[db][4 * j + 3] * f};
+            *(pa_f4 *) (dst + 32 * db + 8 * j + 4 * h2) = v;
+        }
+    if (h2 == 0) {
+        if (direct) {
+            a.m[(size_t) h * a.rows + row] = mx == -INFINITY ? -INFINITY : mx * PA_LN2;
+            a.l[(size_t) h * a.rows + row] = lt * f;
+        } else {
+            a.pml[((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row] = make_float2(mx, lt * f);
+        }
+    }
+}
+
 // PRE: PA_QMODE_GGML over quantized K. Q' then carries scale * log2 e inside its one fp16 rounding, and the QK
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
@@ -142,30 +243,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     const uint32_t row = rb * (32 * NW) + 32 * wave + n;             // this lane's query row (within the KV head)
     const bool rlive = row < a.rows;
 
-    // ---- page cursors (scalar): the page holding a tile, its tile range and key count; a cursor moves only when a tile
-    // leaves its page, so the common case reads no kernel argument memory (whose scalar loads would also wait for the
-    // LDS operations in flight)
-    struct Cursor { uint32_t pg, tb, te, nk; const uint8_t * kb, * vb; };
-    auto cursor0 = [&]() { return Cursor{0u, a.cstart[0], a.cstart[1], a.pstart[1] - a.pstart[0], a.kp[0], a.vp[0]}; };
-    auto seek = [&](Cursor & cu, uint32_t tau) {
-        while (tau >= cu.te) {
-            cu.pg++;
-            cu.tb = cu.te;
-            cu.te = a.cstart[cu.pg + 1];
-            cu.nk = a.pstart[cu.pg + 1] - a.pstart[cu.pg];
-            cu.kb = a.kp[cu.pg];
-            cu.vb = a.vp[cu.pg];
-            __builtin_amdgcn_s_waitcnt(0xc07f);                      // lgkmcnt(0): no scalar load left outstanding
-        }
-    };
-    Cursor cl = cursor0(), cc = cursor0();                           // the next tile to load / to compute
+    MmCursor cl, cc;                                                 // the next tile to load / to compute
+    cl.init(a); cc.init(a);
 
     // ---- staging units of this thread: u = tid + NT*i -> tensor u >> 8 (= (wave + NW*i) >> 2, uniform), key
     // (u >> 3) & 31, block (u >> 1) & 3, half u & 1; rows past the page's end reload its last row (masked later)
     using F = MmFmt<FMT>;
     MmRaw<FMT> R[UPT];
     auto load_tile = [&](uint32_t tau) {
-        seek(cl, tau);
+        cl.seek(a, tau);
         const uint32_t j0 = 32 * (tau - cl.tb);
         const uint32_t last = cl.nk - 1 - j0;
         #pragma unroll
@@ -196,54 +282,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     load_tile(t0);
     __builtin_amdgcn_sched_barrier(0);
     mm_h8 Qf[8];
-    {
-        const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * MM_HD + 8 * h2;
-        const uint32_t qmask = rlive ? 0xffffffffu : 0u;
-        pa_f4 x[16];
-        #pragma unroll
-        for (int kk = 0; kk < 8; kk++) {
-            x[2 * kk] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 16 * kk)) & qmask);
-            x[2 * kk + 1] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 16 * kk + 4)) & qmask);
-        }
-        const float scale = a.scale;
-        if constexpr (PRE) {                                         // PA_QMODE_GGML, quantized K: Q -> q8_0
-            // ggml q8_0 per 32-block b = k-steps 2b, 2b+1: this lane holds 16 of its values, lane ^ 32 the other 16
-            #pragma clang fp contract(off)
-            #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                float am = 0.0f;
-                #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const pa_f4 v = x[4 * b + j];
-                    am = fmaxf(am, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-                }
-                am = mm_max32(am);
-                const float d = am / 127.0f;
-                const float id = d != 0.0f ? 1.0f / d : 0.0f;
-                const float dq = (float) (_Float16) d * (scale * MM_LOG2E);   // the fp16 block scale (as ggml stores it)
-                                                                              // * scale, in base-2 units
-                #pragma unroll
-                for (int kq = 0; kq < 2; kq++) {
-                    mm_h8 f;
-                    #pragma unroll
-                    for (int t = 0; t < 8; t++) {
-                        const float xv = x[4 * b + 2 * kq + t / 4][t % 4];
-                        f[t] = (_Float16) (roundf(xv * id) * dq);
-                    }
-                    Qf[2 * b + kq] = f;
-                }
-            }
-        } else {                                                     // f16(q * scale), or f16(q) for f16 K in
-            const float qs = a.qmode == 0 ? 1.0f : scale;             // PA_QMODE_GGML (ggml's f16 vec_dot type)
-            #pragma unroll
-            for (int kk = 0; kk < 8; kk++) {
-                mm_h8 f;
-                #pragma unroll
-                for (int t = 0; t < 8; t++) f[t] = (_Float16) pa_f32(x[2 * kk + t / 4][t % 4] * qs);   // f2h(q * scale)
-                Qf[kk] = f;
-            }
-        }
-    }
+    mm_prep_q<FMT, PRE>(a, h, row, rlive, h2, Qf);
 
     // ---- prologue: tile t0 -> stage 0, tile t0 + 1's loads in flight
     store_tile(0);
@@ -263,11 +302,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     for (uint32_t t = 0; t < ntiles; t++) {
         const int stage = t & 1;
         const uint32_t tau = t0 + t;
-        seek(cc, tau);                                               // before any LDS operation of this step
+        cc.seek(a, tau);                                             // before any LDS operation of this step
         const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
         // the next tile's bytes -> the other stage (last read before the previous barrier), then the one after's loads
         if (t + 1 < ntiles) {
-            if (t + 2 < ntiles) seek(cl, tau + 2);
+            if (t + 2 < ntiles) cl.seek(a, tau + 2);
             store_tile(stage ^ 1);
             if (t + 2 < ntiles) load_tile(tau + 2);
         }
@@ -341,28 +380,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         mm_lds_barrier();                                            // this stage is free; the next one is written
     }
 
-    // ---- row n: the sum over both lanes; O rebased from the reference max to the exact one
-    const float lt = mm_sum32(lsum);
-    const float f = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mx);
-    if (!rlive) return;
-    const bool direct = a.n_chunks == 1 && a.fused;
-    float * dst = direct ? a.O + ((size_t) h * a.rows + row) * MM_HD
-                         : a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row) * MM_HD;
-    #pragma unroll
-    for (int db = 0; db < 4; db++)
-        #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const pa_f4 v = {O[db][4 * j] * f, O[db][4 * j + 1] * f, O[db][4 * j + 2] * f, O[db][4 * j + 3] * f};
-            *(pa_f4 *) (dst + 32 * db + 8 * j + 4 * h2) = v;
-        }
-    if (h2 == 0) {
-        if (direct) {
-            a.m[(size_t) h * a.rows + row] = mx == -INFINITY ? -INFINITY : mx * PA_LN2;
-            a.l[(size_t) h * a.rows + row] = lt * f;
-        } else {
-            a.pml[((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row] = make_float2(mx, lt * f);
-        }
-    }
+    mm_write_out(a, O, mref, mx, lsum, h, row, rlive, h2, c);
 }
 
 template <int FMT, bool PRE>
