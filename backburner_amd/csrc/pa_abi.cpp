@@ -273,8 +273,9 @@ int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_page
     const uint32_t tile = 32;
     const uint32_t nrb = (s->rows + 32 * nw - 1) / (32 * nw), qr = nrb * 32 * nw;
     const uint32_t units = s->nkv * nrb;
-    // key chunks: about PA_HIP_MMA_TARGET workgroups in all (resident ones: 1 of 8 waves, 2 of 4, 4 of 2 per CU)
-    const int target = std::max(1, env_int("PA_HIP_MMA_TARGET", nw == 8 ? 512 : 1024));
+    // key chunks: about PA_HIP_MMA_TARGET workgroups in all; by default one round of resident ones (1 of 8 waves, 2 of
+    // 4, 4 of 2 per CU, 256 CUs): a second, partial round costs more than the extra slots save
+    const int target = std::max(1, env_int("PA_HIP_MMA_TARGET", 256 * 8 / (int) nw));
     struct launch_t { int p0, np; uint32_t tpc, n_chunks, slot0; };
     std::vector<launch_t> L;
     uint32_t n_slots = 0;
