@@ -143,3 +143,29 @@ def test_decode_128k_full_size(ws):
     eo, em, el = orc.rel_err(O, ml[:nkv * rows], ml[nkv * rows:], *ref)
     print("decode 128k parity", eo, em, el)
     assert eo < TOL and em < TOL and el < TOL, (eo, em, el)
+
+
+@pytest.mark.parametrize("rows", [8, 128])
+def test_page_above_2p20_keys(ws, rows):
+    """One page of 2^20 + 100 keys: the decode path splits it on the host (its per-tile buffer ranges are 32-bit byte
+    counts); the MMA path walks it with 64-bit offsets. Both against the oracle on the same bytes."""
+    nkv, hd, nk = 2, 128, (1 << 20) + 100
+    print(f"page above 2^20 keys rows={rows}", flush=True)
+    rs = nkv * bb.head_bytes(bb.FMT_Q8_0, hd)
+    syn = bb.synth()
+    kbuf, vbuf = bb.DeviceBuffer(nk * rs), bb.DeviceBuffer(nk * rs)
+    assert syn.pa_synth_fill_rows(kbuf.ptr, 1, nkv, hd, rs, 0, nk, 2001, 1.0, 0, None, 1.0, None) == 0
+    assert syn.pa_synth_fill_rows(vbuf.ptr, 1, nkv, hd, rs, 0, nk, 2002, 1.0, 0, None, 1.0, None) == 0
+    bb.device_sync()
+    Q = orc.normal(2003 + rows, 0, nkv * rows * hd).reshape(nkv * rows, hd)
+    pages = bb.Pages([kbuf.ptr], [vbuf.ptr], [nk], [])
+    dq = bb.DeviceBuffer.from_array(Q)
+    do, dml = bb.DeviceBuffer(nkv * rows * hd * 4), bb.DeviceBuffer(nkv * rows * 8)
+    ws.attn(bb.make_shape(nkv, rows, hd, bb.FMT_Q8_0), pages, dq.ptr, do.ptr, dml.ptr, dml.ptr + nkv * rows * 4)
+    bb.device_sync()
+    O = do.download(np.float32).reshape(-1, hd)
+    ml = dml.download(np.float32)
+    ref = orc.attn_ggml(orc.make_shape(nkv, rows, hd, orc.Q8_0), Q, kbuf.download(np.uint8), vbuf.download(np.uint8), nk)
+    eo, em, el = orc.rel_err(O, ml[:nkv * rows], ml[nkv * rows:], *ref)
+    print("page above 2^20 parity", eo, em, el)
+    assert eo < TOL and em < TOL and el < TOL, (eo, em, el)
