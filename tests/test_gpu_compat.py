@@ -1,6 +1,8 @@
 """GPU: the reference's C ABI exported by libpa_hip.so (sme_attn_partial / sme_attn_pipe, phone-attn.h:63-71) with host
-buffers at the reference shape (48 rows per KV head, head dim 256), and the reference's own pa-tool, compiled unchanged
-and linked against libpa_hip.so, running its loopback fp64 check on the GPU engine."""
+buffers at the reference shape (48 rows per KV head, head dim 256); the reference's own pa-tool, compiled unchanged
+and linked against libpa_hip.so, running its loopback fp64 check on the GPU engine; and the reference's unchanged
+pa::server with the product's HIP pa::engine (oracle/_ref/pa-hip-serve), driven over the PATN wire by the unchanged
+pa-tool client with every page on the GPU."""
 import re
 from pathlib import Path
 
@@ -14,6 +16,8 @@ from tests.test_ref_patool import check_line, run_patool
 pytestmark = pytest.mark.gpu
 ROOT = Path(__file__).resolve().parents[1]
 TOOL_HIP = ROOT / "oracle" / "_ref" / "pa-tool-hip"
+TOOL_CPU = ROOT / "oracle" / "_ref" / "pa-tool-cpu"
+SERVE_HIP = ROOT / "oracle" / "_ref" / "pa-hip-serve"
 NR, HD = 48, 256
 
 
@@ -88,4 +92,29 @@ def test_reference_patool_on_gpu_engine(nkeys, ntok):
 @needs_tool
 def test_reference_patool_big_on_gpu_engine():
     out = run_patool(TOOL_HIP, [4096, 2, 2], {"PA_BIG_TOK": 16})
+    assert re.search(r"big vs one-group calls: .* -> PASS", out), out
+
+
+needs_serve = pytest.mark.skipif(not (SERVE_HIP.exists() and TOOL_CPU.exists()),
+                                 reason="oracle/_ref/pa-hip-serve not built (reference checkout absent at build time)")
+
+
+@needs_serve
+@pytest.mark.parametrize("q4,nkeys,ntok", [(0, 16384, 8), (1, 16384, 8), (0, 20480, 1)])
+def test_wire_server_with_hip_engine(q4, nkeys, ntok):
+    """pa-hip-serve (unchanged pa::server + the HIP pa::engine) answering the unchanged pa-tool client: gpu_permille 1000
+    puts every page on the engine; pa-tool's fp64 gate (5e-3) on the normalised reply, held here to 2e-3."""
+    print(f"wire server q4={q4} nkeys={nkeys} ntok={ntok}", flush=True)
+    out = run_patool(TOOL_CPU, [nkeys, 3, 2, 1, 1, 1000, 1024], {"PA_Q4": q4, "PA_NTOK": ntok}, server=SERVE_HIP)
+    print(out)
+    eo, el, verdict = check_line(out)
+    assert verdict == "PASS" and eo < 2e-3 and el < 2e-3, out
+    m = re.search(r"check call: (\d+) of (\d+) pages on the GPU", out)
+    assert m and m.group(1) == m.group(2) and int(m.group(1)) == (nkeys + 4095) // 4096, out
+
+
+@needs_serve
+def test_wire_server_big_calls():
+    """ATTN_BIG (16 tokens = 2 groups in one engine call) against one-group calls, through the HIP engine."""
+    out = run_patool(TOOL_CPU, [16384, 2, 2, 1, 1, 1000, 1024], {"PA_BIG_TOK": 16}, server=SERVE_HIP)
     assert re.search(r"big vs one-group calls: .* -> PASS", out), out

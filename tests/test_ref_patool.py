@@ -4,6 +4,8 @@ oracle's restatement of scripts/sme/sme_attn.c), so pa-tool's fp64 check (pa-too
 its ATTN_BIG vs one-group check (pa-tool.cpp:214-243) pin that restatement at the reference shape (4 KV heads, 48 rows,
 head dim 256, q8_0 rows from pa-tool's own generator). The same binary linked against libpa_hip.so runs in
 tests/test_gpu_compat.py."""
+from __future__ import annotations
+
 import os
 import re
 import socket
@@ -25,11 +27,13 @@ def free_port() -> int:
     return p
 
 
-def run_patool(tool: Path, args: list, env_extra: dict, timeout: int = 600) -> str:
-    """Start `tool serve` on a free loopback port, run `tool test 127.0.0.1 port ...args`, stop the server."""
+def run_patool(tool: Path, args: list, env_extra: dict, timeout: int = 600, server: Path | None = None) -> str:
+    """Start `tool serve` (or `server PORT 2`) on a free loopback port, run `tool test 127.0.0.1 port ...args`, stop the
+    server."""
     port = free_port()
     env = dict(os.environ, **{k: str(v) for k, v in env_extra.items()})
-    srv = subprocess.Popen([str(tool), "serve", str(port), "2"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, env=env)
+    cmd = [str(server), str(port), "2"] if server else [str(tool), "serve", str(port), "2"]
+    srv = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, env=env)
     try:
         for _ in range(100):
             try:
