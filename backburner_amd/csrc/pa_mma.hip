@@ -68,6 +68,22 @@ __device__ __forceinline__ void mm_load_unit(MmRaw<FMT> & r, const uint8_t * blk
     }
 }
 
+// The same unit through a buffer resource (the tile's scalar base, its valid bytes as the range) and a 32-bit offset
+template <int FMT>
+__device__ __forceinline__ void mm_load_unit_buf(MmRaw<FMT> & r, __amdgpu_buffer_rsrc_t rsrc, uint32_t off, int half) {
+    if constexpr (FMT == 1) {
+        r.q[0] = __builtin_bit_cast(pa_u4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 2 + 16 * half, 0, 0));
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+    } else if constexpr (FMT == 2) {
+        r.q[0] = __builtin_bit_cast(pa_u4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 2, 0, 0));
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+    } else {
+        r.q[0] = __builtin_bit_cast(pa_u4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 32 * half, 0, 0));
+        r.q[1] = __builtin_bit_cast(pa_u4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 32 * half + 16, 0, 0));
+        r.d = 0;
+    }
+}
+
 // 16 values -> fp16 (8 dwords). Quantized formats: byte u (unsigned quant) -> fp16 bits 0x6400 | u = 1024 + u exactly,
 // minus (1024 + bias) exactly, times d (one rounding).
 template <int FMT>
@@ -250,6 +266,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     // (u >> 3) & 31, block (u >> 1) & 3, half u & 1; rows past the page's end reload its last row (masked later)
     using F = MmFmt<FMT>;
     MmRaw<FMT> R[UPT];
+    // buffer loads: the tile's first row of this head as the scalar base, its rows up to the page's end as the range
     auto load_tile = [&](uint32_t tau) {
         cl.seek(a, tau);
         const uint32_t j0 = 32 * (tau - cl.tb);
@@ -258,9 +275,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         for (int i = 0; i < UPT; i++) {
             const int u = tid + NT * i;
             const int tensor = (wave + NW * i) >> 2, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
-            const uint8_t * base = (tensor ? cl.vb : cl.kb) + (size_t) h * a.hb;
-            const uint32_t r = j0 + min((uint32_t) key, last);
-            mm_load_unit<FMT>(R[i], base + (size_t) r * a.rs + blk * F::BB, half);
+            const uint8_t * base = (tensor ? cl.vb : cl.kb) + (size_t) h * a.hb + (size_t) j0 * a.rs;
+            const __amdgpu_buffer_rsrc_t rsrc =
+                __builtin_amdgcn_make_buffer_rsrc((void *) base, (short) 0, (int) ((last + 1) * a.rs), 0x00020000);
+            mm_load_unit_buf<FMT>(R[i], rsrc, min((uint32_t) key, last) * a.rs + blk * F::BB, half);
         }
     };
     auto store_tile = [&](int stage) {
