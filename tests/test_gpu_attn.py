@@ -169,3 +169,32 @@ def test_page_above_2p20_keys(ws, rows):
     eo, em, el = orc.rel_err(O, ml[:nkv * rows], ml[nkv * rows:], *ref)
     print("page above 2^20 parity", eo, em, el)
     assert eo < TOL and em < TOL and el < TOL, (eo, em, el)
+
+
+@pytest.mark.parametrize("fmt,rows,nk,outliers", [(bb.FMT_Q8_0, 128, 98304, 0), (bb.FMT_Q4_0, 8, 143360, 0),
+                                                  (bb.FMT_Q4_0, 128, 143360, 0)])
+def test_full_size_verify_and_q4(ws, fmt, rows, nk, outliers):
+    """The other full-size workloads: 16-token verify over 98,304 q8_0 keys, and 1-token decode / 16-token verify over
+    143,360 q4_0 keys (8 KV heads, GQA 8, pages of 4096), GPU-made pages checked against the oracle on the same bytes."""
+    nkv, hd = 8, 128
+    print(f"full size fmt={fmt} rows={rows} nk={nk}", flush=True)
+    rs = nkv * bb.head_bytes(fmt, hd)
+    syn = bb.synth()
+    kbuf, vbuf = bb.DeviceBuffer(nk * rs), bb.DeviceBuffer(nk * rs)
+    assert syn.pa_synth_fill_rows(kbuf.ptr, fmt, nkv, hd, rs, 0, nk, 3001 + fmt, 1.0, 0, None, 1.0, None) == 0
+    assert syn.pa_synth_fill_rows(vbuf.ptr, fmt, nkv, hd, rs, 0, nk, 3002 + fmt, 1.0, 0, None, 1.0, None) == 0
+    bb.device_sync()
+    Q = orc.normal(3003 + rows, 0, nkv * rows * hd).reshape(nkv * rows, hd)
+    npg = nk // 4096
+    pages = bb.Pages([kbuf.ptr + i * 4096 * rs for i in range(npg)], [vbuf.ptr + i * 4096 * rs for i in range(npg)],
+                     [4096] * npg, [])
+    dq = bb.DeviceBuffer.from_array(Q)
+    do, dml = bb.DeviceBuffer(nkv * rows * hd * 4), bb.DeviceBuffer(nkv * rows * 8)
+    ws.attn(bb.make_shape(nkv, rows, hd, fmt), pages, dq.ptr, do.ptr, dml.ptr, dml.ptr + nkv * rows * 4)
+    bb.device_sync()
+    O = do.download(np.float32).reshape(-1, hd)
+    ml = dml.download(np.float32)
+    ref = orc.attn_ggml(orc.make_shape(nkv, rows, hd, fmt), Q, kbuf.download(np.uint8), vbuf.download(np.uint8), nk)
+    eo, em, el = orc.rel_err(O, ml[:nkv * rows], ml[nkv * rows:], *ref)
+    print("full size parity", fmt, rows, nk, eo, em, el)
+    assert eo < TOL and em < TOL and el < TOL, (eo, em, el)
