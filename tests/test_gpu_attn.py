@@ -171,12 +171,14 @@ def test_page_above_2p20_keys(ws, rows):
     assert eo < TOL and em < TOL and el < TOL, (eo, em, el)
 
 
-@pytest.mark.parametrize("fmt,rows,nk,outliers", [(bb.FMT_Q8_0, 128, 98304, 0), (bb.FMT_Q4_0, 8, 143360, 0),
-                                                  (bb.FMT_Q4_0, 128, 143360, 0)])
-def test_full_size_verify_and_q4(ws, fmt, rows, nk, outliers):
+@pytest.mark.parametrize("fmt,rows,nk,nkv", [(bb.FMT_Q8_0, 128, 98304, 8), (bb.FMT_Q4_0, 8, 143360, 8),
+                                             (bb.FMT_Q4_0, 128, 143360, 8), (bb.FMT_Q8_0, 4096, 4096, 8),
+                                             (bb.FMT_Q8_0, 4096, 65536, 1)])
+def test_full_size_verify_and_q4(ws, fmt, rows, nk, nkv):
     """The other full-size workloads: 16-token verify over 98,304 q8_0 keys, and 1-token decode / 16-token verify over
-    143,360 q4_0 keys (8 KV heads, GQA 8, pages of 4096), GPU-made pages checked against the oracle on the same bytes."""
-    nkv, hd = 8, 128
+    143,360 q4_0 keys (8 KV heads, GQA 8, pages of 4096); the prefill chunk's 4096 rows per KV head over one page of 8
+    heads, and over the full 65,536 keys for one head. GPU-made pages checked against the oracle on the same bytes."""
+    hd = 128
     print(f"full size fmt={fmt} rows={rows} nk={nk}", flush=True)
     rs = nkv * bb.head_bytes(fmt, hd)
     syn = bb.synth()
