@@ -4,11 +4,13 @@
 // block verification, serve.sh:300-302). Semantics: a_i = argmax_j logits[i][j] with the lowest index on ties (numpy's
 // rule, which also makes the first NaN win); k = the longest prefix with a_i == draft_i (i < n_rows-1); bonus = a_k.
 //
-// Layout: n_rows x splits workgroups, each scans one contiguous slice of one row with 16-byte loads and reduces a 64-bit
-// key (orderable value << 32 | ~index) so that one unsigned max picks the largest value and, among equal values, the
-// lowest index. Each workgroup publishes its key; the last one to finish (device-scope counter, no waiting) folds the
-// row keys and computes (k, bonus). The counter is reset by that last workgroup, so no memset is needed between calls.
-// Only that workgroup acquires at device scope (an L2 invalidate); the others only release their key.
+// Layout: n_rows x splits workgroups; workgroup (row, sp) scans values [4096 sp, 4096 sp + 4096) of its row, every
+// thread issuing all its loads at once (four 16-byte loads, or sixteen scalar ones when the vocab is not a multiple
+// of 4), and reduces a 64-bit key (orderable value << 32 | ~index) so that one unsigned max picks the largest value
+// and, among equal values, the lowest index. Each workgroup publishes its key with a write-through store and waits for
+// it to complete before it counts itself done on a device-scope counter; the last one reads the keys with
+// write-through loads, folds them per row and computes (k, bonus). No cache write-back or invalidate is needed: the
+// keys never sit in an XCD's L2. The last workgroup resets the counter, so no memset is needed between calls.
 #include "pa_attn.h"
 #include "pa_common.h"
 
@@ -25,49 +27,81 @@ __device__ __forceinline__ unsigned long long accept_key(float x, uint32_t idx) 
     return ((unsigned long long) k << 32) | (unsigned long long) (0xffffffffu - idx);
 }
 
+constexpr int64_t ACCEPT_SEG = 4096;                                 // values per workgroup
+
 __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
 
 __global__ __launch_bounds__(256) void accept_kernel(const AcceptArgs a) {
     __shared__ unsigned long long red[4];
     __shared__ bool last;
     const int row = blockIdx.x / a.splits, sp = blockIdx.x % a.splits;
-    const int64_t seg = ((a.vocab + a.splits - 1) / a.splits + 3) / 4 * 4;
-    const int64_t j0 = (int64_t) sp * seg, j1 = min(a.vocab, j0 + seg);
+    const int64_t j0 = (int64_t) sp * ACCEPT_SEG, j1 = min(a.vocab, j0 + ACCEPT_SEG);
     const float * x = a.logits + (size_t) row * (size_t) a.vocab;
     unsigned long long best = 0;
     const int t = threadIdx.x;
-    if ((a.vocab & 3) == 0) {
-        for (int64_t j = j0 + 4 * t; j < j1; j += 4 * 256) {
-            const pa_f4 v = *(const pa_f4 *) (x + j);
-            best = umax64(best, accept_key(v[0], (uint32_t) j));
-            best = umax64(best, accept_key(v[1], (uint32_t) (j + 1)));
-            best = umax64(best, accept_key(v[2], (uint32_t) (j + 2)));
-            best = umax64(best, accept_key(v[3], (uint32_t) (j + 3)));
+    if ((a.vocab & 3) == 0) {                                        // j < j1 implies j + 3 < vocab
+        pa_f4 v[4];
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int64_t j = j0 + 4 * t + 1024 * u;
+            v[u] = j < j1 ? *(const pa_f4 *) (x + j) : (pa_f4){0.f, 0.f, 0.f, 0.f};
+        }
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int64_t j = j0 + 4 * t + 1024 * u;
+            if (j < j1) {
+                #pragma unroll
+                for (int e = 0; e < 4; e++) best = umax64(best, accept_key(v[u][e], (uint32_t) (j + e)));
+            }
         }
     } else {
-        for (int64_t j = j0 + t; j < j1; j += 256) best = umax64(best, accept_key(x[j], (uint32_t) j));
+        float v[16];
+        #pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int64_t j = j0 + t + 256 * u;
+            v[u] = j < j1 ? x[j] : 0.0f;
+        }
+        #pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int64_t j = j0 + t + 256 * u;
+            if (j < j1) best = umax64(best, accept_key(v[u], (uint32_t) j));
+        }
     }
     for (int off = 32; off > 0; off >>= 1) best = umax64(best, __shfl_xor(best, off));
     if ((t & 63) == 0) red[t / 64] = best;
     __syncthreads();
     if (t == 0) {
         best = umax64(umax64(red[0], red[1]), umax64(red[2], red[3]));
+        // write-through store (device scope), complete before the count below is made
         __hip_atomic_store(&a.part[row * a.splits + sp], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // release at device scope (one L2 write-back); only the completing workgroup acquires (invalidates)
-        const unsigned int done = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        const unsigned int done = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = done == (unsigned int) (a.n_rows * a.splits - 1);
     }
     __syncthreads();
     if (!last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // the last workgroup: fold each row's keys, then the accepted prefix
+    // the last workgroup: every thread reads a share of all keys at once (write-through loads) and folds them into
+    // its row's slot (LDS atomic max), then the accepted prefix
+    __shared__ unsigned long long rk[64];
     __shared__ int32_t am[64];
-    if (t < a.n_rows) {
-        unsigned long long b = 0;
-        for (int s = 0; s < a.splits; s++)
-            b = umax64(b, __hip_atomic_load(&a.part[t * a.splits + s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        am[t] = (int32_t) (0xffffffffu - (uint32_t) (b & 0xffffffffu));
+    if (t < a.n_rows) rk[t] = 0;
+    __syncthreads();
+    const int nk = a.n_rows * a.splits;
+    for (int i0 = 0; i0 < nk; i0 += 4 * 256) {
+        unsigned long long k4[4];
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + t + 256 * u;
+            k4[u] = i < nk ? __hip_atomic_load(&a.part[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        }
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + t + 256 * u;
+            if (i < nk) __hip_atomic_fetch_max(&rk[i / a.splits], k4[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
     }
+    __syncthreads();
+    if (t < a.n_rows) am[t] = (int32_t) (0xffffffffu - (uint32_t) (rk[t] & 0xffffffffu));
     __syncthreads();
     if (t == 0) {
         int k = 0;
