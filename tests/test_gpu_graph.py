@@ -71,3 +71,41 @@ def test_graph_replays_match_eager(fmt, nkv, rows, hd, nk, qmode, reply):
             syn.pa_synth_graph_free(gx)
         ws.close()
         pages.close()
+
+
+def test_graph_replays_accept():
+    """pa_hip_accept captured in a graph (its completion counter is reset by the kernel itself, no memset): every replay
+    over poisoned output equals the eager call, and the counter stays usable for the eager calls in between."""
+    print("graph accept", flush=True)
+    syn = bb.synth()
+    rng = np.random.default_rng(44)
+    logits = rng.standard_normal((17, 151936)).astype(np.float32)
+    draft = rng.integers(0, 151936, 16).astype(np.int32)
+    for i in range(6):
+        logits[i, draft[i]] = logits[i].max() + 1.0
+    dl, dd, do = bb.DeviceBuffer.from_array(logits), bb.DeviceBuffer.from_array(draft), bb.DeviceBuffer(19 * 4)
+    ws = bb.Workspace()
+    stream = syn.pa_synth_stream_new()
+    gx = None
+    try:
+        ws.accept(dl.ptr, 17, 151936, dd.ptr, do.ptr, stream)
+        assert syn.pa_synth_stream_sync(stream) == 0
+        want = do.download(np.int32)
+        k, bonus, am = orc.accept(logits, draft)
+        assert want[0] == k == 6 and want[1] == bonus and np.array_equal(want[2:], am)
+        assert syn.pa_synth_capture_begin(stream) == 0
+        ws.accept(dl.ptr, 17, 151936, dd.ptr, do.ptr, stream)
+        gx = syn.pa_synth_capture_end(stream)
+        assert gx, "capture failed"
+        for rep in range(4):
+            do.upload(np.full(19, -7, np.int32))
+            assert syn.pa_synth_graph_launch(gx, stream) == 0
+            assert syn.pa_synth_stream_sync(stream) == 0
+            assert np.array_equal(do.download(np.int32), want), f"replay {rep}"
+            ws.accept(dl.ptr, 17, 151936, dd.ptr, do.ptr, stream)
+            assert syn.pa_synth_stream_sync(stream) == 0
+            assert np.array_equal(do.download(np.int32), want)
+    finally:
+        if gx:
+            syn.pa_synth_graph_free(gx)
+        ws.close()
