@@ -250,18 +250,17 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     };
 
     // ---- the query rows' loads first, then the first two tiles' loads, so that the query preparation waits only for
-    // its own loads (memory counters are in order). Lane (g, n): row n % 8 (row 0 when past the rows, then zeroed),
-    // elements 16*(g%2) .. +15 of every block.
-    const int qr8 = n & 7;
-    const bool qlive = qr8 < (int) a.rows;
+    // its own loads (memory counters are in order). Each lane takes one (row, block, half): lane 8 r + 2 b + e holds
+    // elements 32 b + 16 e .. +15 of row r (row 0 when past the rows, then zeroed), so every query value is quantized
+    // once, and the two halves of a block sit in neighbouring lanes.
+    const int qrl = lane >> 3, qbl = (lane >> 1) & 3, qhl = lane & 1;
+    const bool qlive = qrl < (int) a.rows;
     const uint32_t qmask = qlive ? 0xffffffffu : 0u;
-    pa_f4 qx[DEC_NKB][4];
+    pa_f4 qx[4];
     {
-        const float * qrow = a.q + ((size_t) h * a.rows + (qlive ? qr8 : 0)) * DEC_HD + 16 * hh;
+        const float * qp = a.q + ((size_t) h * a.rows + (qlive ? qrl : 0)) * DEC_HD + 32 * qbl + 16 * qhl;
         #pragma unroll
-        for (int b = 0; b < DEC_NKB; b++)
-            #pragma unroll
-            for (int j = 0; j < 4; j++) qx[b][j] = *(const pa_f4 *) (qrow + 32 * b + 4 * j);
+        for (int j = 0; j < 4; j++) qx[j] = *(const pa_f4 *) (qp + 4 * j);
     }
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t ntiles = (T - c + NG - 1) / NG;                   // >= 1: c < NG <= T
@@ -286,47 +285,42 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- query rows: ggml's q8_0 of each 32-block (d = amax/127, id = 1/d, q = roundf(x*id), d -> fp16;
-    // quantize_row_q8_0_ref), kept in the wave's LDS table and read per tile as the int8 A operand: lane (g, n) takes
-    // row slot n (row n % 8; slots 8-15 face keys 16-31), bytes 16*(g%2) .. +15 of the block, or the zero slot unless
-    // g / 2 == n / 8. Beside it: the fp16 query scale * s_mul per (block, row), and for q4_0 K the MFMA accumulator start
-    // -8 * (sum of the row's block quants).
+    // quantize_row_q8_0_ref), kept in the wave's LDS table [block][row][half][16 bytes] + a zero slot and read per tile
+    // as the int8 A operand: lane (g, n) takes row slot n (row n % 8; slots 8-15 face keys 16-31), bytes 16*(g%2) .. +15
+    // of the block, or the zero slot unless g / 2 == n / 8. Beside it: the fp16 query scale * s_mul per (block, row), and
+    // for q4_0 K the MFMA accumulator start -8 * (sum of the row's block quants).
     {
         #pragma clang fp contract(off)
+        float x[16];
         #pragma unroll
-        for (int b = 0; b < DEC_NKB; b++) {
-            float x[16];
-            #pragma unroll
-            for (int j = 0; j < 4; j++) {                            // a dead row is zeroed by a mask, so that the loads
-                // stay where they were issued (whole vectors are bit-cast: clang's bit_cast of one ext-vector element
-                // reads element 0)
-                const pa_f4 v = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, qx[b][j]) & qmask);
-                x[4 * j] = v[0]; x[4 * j + 1] = v[1]; x[4 * j + 2] = v[2]; x[4 * j + 3] = v[3];
-            }
-            float am = 0.0f;
-            #pragma unroll
-            for (int j = 0; j < 16; j++) am = fmaxf(am, fabsf(x[j]));
-            am = fmaxf(am, __shfl_xor(am, 16));                      // the other half of the block: lane ^ 16
-            const float d = am / 127.0f;
-            const float id = d != 0.0f ? 1.0f / d : 0.0f;
-            uint32_t wq[4] = {0, 0, 0, 0};
-            int qsum = 0;
-            #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float t = x[j] * id;
-                const int q = (int) roundf(t);
-                qsum += q;
-                wq[j / 4] |= ((uint32_t) q & 0xffu) << (8 * (j % 4));
-            }
-            qsum += __shfl_xor(qsum, 16);
-            if (g < 2 && n < 8) {                                    // (row n, half g) for every block
-                *(pa_u4 *) (Qt + b * DEC_QBLK + n * 32 + g * 16) = (pa_u4){wq[0], wq[1], wq[2], wq[3]};
-                if (g == 0) {
-                    Ct[b * 8 + n] = (float) (_Float16) d * a.s_mul;
-                    Ct[DEC_NKB * 8 + b * 8 + n] = __builtin_bit_cast(float, -8 * qsum);
-                }
-            }
-            if (lane == 0) *(pa_u4 *) (Qt + b * DEC_QBLK + 256) = (pa_u4){0u, 0u, 0u, 0u};
+        for (int j = 0; j < 4; j++) {                                // a dead row is zeroed by a mask, so that the loads
+            // stay where they were issued (whole vectors are bit-cast: clang's bit_cast of one ext-vector element reads
+            // element 0)
+            const pa_f4 v = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, qx[j]) & qmask);
+            x[4 * j] = v[0]; x[4 * j + 1] = v[1]; x[4 * j + 2] = v[2]; x[4 * j + 3] = v[3];
         }
+        float am = 0.0f;
+        #pragma unroll
+        for (int j = 0; j < 16; j++) am = fmaxf(am, fabsf(x[j]));
+        am = fmaxf(am, dec_dpp<0xb1>(am));                           // the other half of the block: lane ^ 1
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t wq[4] = {0, 0, 0, 0};
+        int qsum = 0;
+        #pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const float t = x[j] * id;
+            const int q = (int) roundf(t);
+            qsum += q;
+            wq[j / 4] |= ((uint32_t) q & 0xffu) << (8 * (j % 4));
+        }
+        qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xb1, 0xf, 0xf, false);
+        *(pa_u4 *) (Qt + qbl * DEC_QBLK + qrl * 32 + qhl * 16) = (pa_u4){wq[0], wq[1], wq[2], wq[3]};
+        if (qhl == 0) {
+            Ct[qbl * 8 + qrl] = (float) (_Float16) d * a.s_mul;
+            Ct[DEC_NKB * 8 + qbl * 8 + qrl] = __builtin_bit_cast(float, -8 * qsum);
+        }
+        if (lane < DEC_NKB) *(pa_u4 *) (Qt + lane * DEC_QBLK + 256) = (pa_u4){0u, 0u, 0u, 0u};
         dec_wave_sync();
     }
     const int qoffa = (g >> 1) == (n >> 3) ? (n & 7) * 32 + hh * 16 : 256;   // this lane's A operand in a block table
