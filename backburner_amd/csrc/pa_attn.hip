@@ -575,15 +575,16 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     }
 }
 
-// Many slots (split-K decode, up to 256): one workgroup per (row, 32 dims), one thread per slot, so that every load
-// of the fold is issued at once (one memory latency, not one per slot): thread t reads slot t's (max, sum) and its 32
-// dims, the workgroup reduces the max and the weighted sums through LDS.
-template <int HD>
-__global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
-    constexpr int NQ = HD / 32;
-    __shared__ float sO[256][33];                   // slot x dim (padded: column sums read conflict-free)
-    __shared__ float sP[8][32];
-    __shared__ float sM[4], sL[4];
+// Many slots (split-K decode up to 256, verify up to 64): one workgroup of NT threads (256, or one wave for at most 64
+// slots) per (row, 32 dims), one thread per slot, so that every load of the fold is issued at once (one memory
+// latency, not one per slot): thread t reads slot t's (max, sum) and its 32 dims, the workgroup reduces the max and
+// the weighted sums through LDS.
+template <int HD, int NT>
+__global__ __launch_bounds__(NT) void merge_wide_kernel(const MergeArgs a) {
+    constexpr int NQ = HD / 32, NWV = NT / 64, NSEG = NT / 32;
+    __shared__ float sO[NT][33];                    // slot x dim (padded: column sums read conflict-free)
+    __shared__ float sP[NSEG][32];
+    __shared__ float sM[NWV], sL[NWV];
     const uint32_t r = blockIdx.x / NQ, dq = blockIdx.x % NQ;   // output row h*rows + i, dims 32 dq .. +31
     const uint32_t h = r / a.rows, i = r % a.rows;
     const int t = threadIdx.x, lane = t % 64, wv = t / 64;
@@ -603,9 +604,12 @@ __global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
     float M = ml.x;
     #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (lane == 0) sM[wv] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(sM[0], sM[1]), fmaxf(sM[2], sM[3]));
+    if constexpr (NWV > 1) {
+        if (lane == 0) sM[wv] = M;
+        __syncthreads();
+        #pragma unroll
+        for (int k = 0; k < NWV; k++) M = fmaxf(M, sM[k]);
+    }
     const float Ms = M == -INFINITY ? 0.0f : M;
     const float w = __builtin_amdgcn_exp2f(ml.x - Ms);              // -inf (an empty or absent slot) -> 0
     float L = w * ml.y;
@@ -617,7 +621,7 @@ __global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
         #pragma unroll
         for (int k = 0; k < 4; k++) sO[t][4 * j + k] = w * o[j][k];
     __syncthreads();
-    {                                                                // column sums over 8 segments of 32 slots
+    {                                                                // column sums over NSEG segments of 32 slots
         const int c = t % 32, seg = t / 32;
         float acc = 0.0f;
         #pragma unroll
@@ -628,15 +632,18 @@ __global__ __launch_bounds__(256) void merge_wide_kernel(const MergeArgs a) {
     if (t < 32) {
         float acc = 0.0f;
         #pragma unroll
-        for (int seg = 0; seg < 8; seg++) acc += sP[seg][t];
+        for (int seg = 0; seg < NSEG; seg++) acc += sP[seg][t];
+        float Lt = 0.0f;
+        #pragma unroll
+        for (int k = 0; k < NWV; k++) Lt += sL[k];
         if (a.Oh) {
-            merge_write_reply<1>(a, (size_t) r * HD + 32 * dq + t, &acc, M, sL[0] + sL[1] + sL[2] + sL[3], r, dq == 0 && t == 0);
+            merge_write_reply<1>(a, (size_t) r * HD + 32 * dq + t, &acc, M, Lt, r, dq == 0 && t == 0);
             return;
         }
         a.O[(size_t) r * HD + 32 * dq + t] = acc;
         if (dq == 0 && t == 0) {
             a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2;
-            a.l[r] = sL[0] + sL[1] + sL[2] + sL[3];
+            a.l[r] = Lt;
         }
     }
 }
@@ -743,9 +750,15 @@ void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
 
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
     const uint32_t grid = a.nkv * a.rows;
-    if (a.n_slots >= 32 && a.n_slots <= 256) {                      // many slots: one thread per slot
-        if (hd == 128) hipLaunchKernelGGL(merge_wide_kernel<128>, dim3(grid * 4), dim3(256), 0, st, a);
-        else if (hd == 256) hipLaunchKernelGGL(merge_wide_kernel<256>, dim3(grid * 8), dim3(256), 0, st, a);
+    if (a.n_slots > 16 && a.n_slots <= 64) {                        // many slots: one thread per slot, one wave
+        if (hd == 128) hipLaunchKernelGGL((merge_wide_kernel<128, 64>), dim3(grid * 4), dim3(64), 0, st, a);
+        else if (hd == 256) hipLaunchKernelGGL((merge_wide_kernel<256, 64>), dim3(grid * 8), dim3(64), 0, st, a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
+    if (a.n_slots > 64 && a.n_slots <= 256) {                       // up to 256: four waves
+        if (hd == 128) hipLaunchKernelGGL((merge_wide_kernel<128, 256>), dim3(grid * 4), dim3(256), 0, st, a);
+        else if (hd == 256) hipLaunchKernelGGL((merge_wide_kernel<256, 256>), dim3(grid * 8), dim3(256), 0, st, a);
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }

@@ -235,7 +235,7 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
 // PRE: PA_QMODE_GGML over quantized K. Q' then carries scale * log2 e inside its one fp16 rounding, and the QK
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
-template <int FMT, int NW, bool PRE>
+template <int FMT, int NW, bool PRE, int PF>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
     constexpr int NT = 64 * NW;
     constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
@@ -265,9 +265,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     // ---- staging units of this thread: u = tid + NT*i -> tensor u >> 8 (= (wave + NW*i) >> 2, uniform), key
     // (u >> 3) & 31, block (u >> 1) & 3, half u & 1; rows past the page's end reload its last row (masked later)
     using F = MmFmt<FMT>;
-    MmRaw<FMT> R[UPT];
+    MmRaw<FMT> R0[UPT], R1[UPT];                                     // tile t's raw bytes in R(t % PF)
     // buffer loads: the tile's first row of this head as the scalar base, its rows up to the page's end as the range
-    auto load_tile = [&](uint32_t tau) {
+    auto load_tile = [&](MmRaw<FMT> (&R)[UPT], uint32_t tau) {
         cl.seek(a, tau);
         const uint32_t j0 = 32 * (tau - cl.tb);
         const uint32_t last = cl.nk - 1 - j0;
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             mm_load_unit_buf<FMT>(R[i], rsrc, min((uint32_t) key, last) * a.rs + blk * F::BB, half);
         }
     };
-    auto store_tile = [&](int stage) {
+    auto store_tile = [&](const MmRaw<FMT> (&R)[UPT], int stage) {
         char * st = smem + stage * MM_STAGE;
         #pragma unroll
         for (int i = 0; i < UPT; i++) {
@@ -296,15 +296,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         }
     };
 
-    // ---- the first tile's loads, then the query rows (B operand: lane (h2, n) holds row n, dims 16kk + 8h2 + t)
-    load_tile(t0);
+    // ---- the first PF tiles' loads, then the query rows (B operand: lane (h2, n) holds row n, dims 16kk + 8h2 + t)
+    load_tile(R0, t0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (PF == 2 && ntiles > 1) load_tile(R1, t0 + 1);
     __builtin_amdgcn_sched_barrier(0);
     mm_h8 Qf[8];
     mm_prep_q<FMT, PRE>(a, h, row, rlive, h2, Qf);
 
-    // ---- prologue: tile t0 -> stage 0, tile t0 + 1's loads in flight
-    store_tile(0);
-    if (ntiles > 1) load_tile(t0 + 1);
+    // ---- prologue: tile t0 -> stage 0, the next tile (PF = 1), or the one after (PF = 2) in flight in R0
+    store_tile(R0, 0);
+    if (ntiles > PF) load_tile(R0, t0 + PF);
     mm_lds_barrier();
 
     mm_f16 O[4];
@@ -317,16 +319,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     const mm_h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
 
     const int q4 = lane >> 4, s4 = lane & 15;
-    for (uint32_t t = 0; t < ntiles; t++) {
+    // one tile step; Rn holds tile t + 1's raw bytes
+    auto step = [&](uint32_t t, MmRaw<FMT> (&Rn)[UPT]) {
         const int stage = t & 1;
         const uint32_t tau = t0 + t;
         cc.seek(a, tau);                                             // before any LDS operation of this step
         const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
-        // the next tile's bytes -> the other stage (last read before the previous barrier), then the one after's loads
+        // the next tile's bytes -> the other stage (last read before the previous barrier), then tile t + 1 + PF's
+        // loads into the registers just freed
         if (t + 1 < ntiles) {
-            if (t + 2 < ntiles) cl.seek(a, tau + 2);
-            store_tile(stage ^ 1);
-            if (t + 2 < ntiles) load_tile(tau + 2);
+            if (t + 1 + PF < ntiles) cl.seek(a, tau + 1 + PF);
+            store_tile(Rn, stage ^ 1);
+            if (t + 1 + PF < ntiles) load_tile(Rn, tau + 1 + PF);
         }
         const char * Kt = smem + stage * MM_STAGE;
         const char * Vt = Kt + MM_KT;
@@ -396,20 +400,36 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             #pragma unroll
             for (int mi = 0; mi < 2; mi++) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][mi], P[mi], O[db], 0, 0, 0);
         mm_lds_barrier();                                            // this stage is free; the next one is written
+    };
+    if constexpr (PF == 1) {
+        for (uint32_t t = 0; t < ntiles; t++) step(t, R0);
+    } else {                                                         // tile t + 1 is in R((t + 1) % 2)
+        uint32_t t = 0;
+        for (; t + 2 <= ntiles; t += 2) {
+            step(t, R1);
+            step(t + 1, R0);
+        }
+        if (t < ntiles) step(t, R1);
     }
 
     mm_write_out(a, O, mref, mx, lsum, h, row, rlive, h2, c);
 }
 
-template <int FMT, bool PRE>
-static hipError_t launch_mma_fmt(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+template <int FMT, bool PRE, int PF>
+static hipError_t launch_mma_pf(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     switch (nw) {
-        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
-        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
+        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE, PF>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
+        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, PF>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, PF>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+template <int FMT, bool PRE>
+static hipError_t launch_mma_fmt(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    static const int pf = getenv("PA_HIP_MMA_PF") && atoi(getenv("PA_HIP_MMA_PF")) == 1 ? 1 : 2;
+    return pf == 1 ? launch_mma_pf<FMT, PRE, 1>(nw, a, grid, st, ev0, ev1) : launch_mma_pf<FMT, PRE, 2>(nw, a, grid, st, ev0, ev1);
 }
 
 hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
