@@ -314,7 +314,8 @@ int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_page
         }
         a.pstart[ln.np] = acc;
         a.cstart[ln.np] = tacc;
-        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.tpc;
+        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks;
+        a.chunk = env_int("PA_HIP_MMA_IL", 0) != 0 ? 0u : ln.tpc;  // 0: chunk c takes tiles c, c + n_chunks, ...
         a.n_items = ln.n_chunks * units;
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale; a.s_mul = 1.4426950408889634f;

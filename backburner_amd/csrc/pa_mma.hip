@@ -250,8 +250,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     if (local >= t8 || w >= a.n_items) return;
     const uint32_t rb = w % a.nrb, h = (w / a.nrb) % a.nkv, c = w / (a.nrb * a.nkv);
     const uint32_t T = a.cstart[a.n_pages];                          // 32-key tiles of the call
-    const uint32_t t0 = c * a.chunk, t1 = min(t0 + a.chunk, T);      // this chunk's tiles [t0, t1)
-    const uint32_t ntiles = t1 - t0;                                  // >= 1
+    // this chunk's tiles t0 + k * ts, k < ntiles: consecutive (a.chunk per chunk), or with a.chunk = 0 interleaved,
+    // chunk c of NC taking tiles c, c + NC, ... (all workgroups stream through one narrow window of the cache)
+    const bool il = a.chunk == 0;
+    const uint32_t t0 = il ? c : c * a.chunk, ts = il ? a.n_chunks : 1u;
+    const uint32_t ntiles = il ? (T - c + ts - 1) / ts : min(t0 + a.chunk, T) - t0;   // >= 1: c < n_chunks <= T
 
     const int tid = threadIdx.x, lane = tid % 64;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
@@ -266,18 +269,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     // (u >> 3) & 31, block (u >> 1) & 3, half u & 1; rows past the page's end reload its last row (masked later)
     using F = MmFmt<FMT>;
     MmRaw<FMT> R0[UPT], R1[UPT];                                     // tile t's raw bytes in R(t % PF)
-    // buffer loads: the tile's first row of this head as the scalar base, its rows up to the page's end as the range
-    auto load_tile = [&](MmRaw<FMT> (&R)[UPT], uint32_t tau) {
-        cl.seek(a, tau);
-        const uint32_t j0 = 32 * (tau - cl.tb);
-        const uint32_t last = cl.nk - 1 - j0;
+    // buffer loads: the tile's first row of this head as the scalar base, its rows up to the page's end as the range.
+    // Past the chunk's last tile (live false) the same loads go out with an empty range (no memory access, zeros), so
+    // that every step issues the same batch and the wait before a tile's dequant covers its own batch only.
+    auto load_tile = [&](MmRaw<FMT> (&R)[UPT], uint32_t tau, bool live) {
+        if (live) cl.seek(a, tau);
+        const uint32_t j0 = live ? 32 * (tau - cl.tb) : 0u;
+        const uint32_t last = live ? cl.nk - 1 - j0 : 0u;
+        const uint32_t nrec = live ? (last + 1) * a.rs : 0u;
         #pragma unroll
         for (int i = 0; i < UPT; i++) {
             const int u = tid + NT * i;
             const int tensor = (wave + NW * i) >> 2, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
             const uint8_t * base = (tensor ? cl.vb : cl.kb) + (size_t) h * a.hb + (size_t) j0 * a.rs;
-            const __amdgpu_buffer_rsrc_t rsrc =
-                __builtin_amdgcn_make_buffer_rsrc((void *) base, (short) 0, (int) ((last + 1) * a.rs), 0x00020000);
+            const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *) base, (short) 0, (int) nrec, 0x00020000);
             mm_load_unit_buf<FMT>(R[i], rsrc, min((uint32_t) key, last) * a.rs + blk * F::BB, half);
         }
     };
@@ -297,16 +302,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     };
 
     // ---- the first PF tiles' loads, then the query rows (B operand: lane (h2, n) holds row n, dims 16kk + 8h2 + t)
-    load_tile(R0, t0);
+    load_tile(R0, t0, true);
     __builtin_amdgcn_sched_barrier(0);
-    if (PF == 2 && ntiles > 1) load_tile(R1, t0 + 1);
+    if constexpr (PF == 2) load_tile(R1, t0 + ts, ntiles > 1);
     __builtin_amdgcn_sched_barrier(0);
     mm_h8 Qf[8];
     mm_prep_q<FMT, PRE>(a, h, row, rlive, h2, Qf);
 
     // ---- prologue: tile t0 -> stage 0, the next tile (PF = 1), or the one after (PF = 2) in flight in R0
     store_tile(R0, 0);
-    if (ntiles > PF) load_tile(R0, t0 + PF);
+    load_tile(R0, t0 + PF * ts, ntiles > PF);
     mm_lds_barrier();
 
     mm_f16 O[4];
@@ -322,16 +327,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     // one tile step; Rn holds tile t + 1's raw bytes
     auto step = [&](uint32_t t, MmRaw<FMT> (&Rn)[UPT]) {
         const int stage = t & 1;
-        const uint32_t tau = t0 + t;
+        const uint32_t tau = t0 + t * ts;
         cc.seek(a, tau);                                             // before any LDS operation of this step
         const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
-        // the next tile's bytes -> the other stage (last read before the previous barrier), then tile t + 1 + PF's
-        // loads into the registers just freed
-        if (t + 1 < ntiles) {
-            if (t + 1 + PF < ntiles) cl.seek(a, tau + 1 + PF);
-            store_tile(Rn, stage ^ 1);
-            if (t + 1 + PF < ntiles) load_tile(Rn, tau + 1 + PF);
-        }
+        // the next tile's bytes -> the other stage (last read before the previous barrier; past the chunk's end the
+        // stage is written and never read), then tile t + 1 + PF's loads into the registers just freed
+        const bool nlive = t + 1 + PF < ntiles;
+        if (nlive) cl.seek(a, tau + (1 + PF) * ts);
+        store_tile(Rn, stage ^ 1);
+        load_tile(Rn, tau + (1 + PF) * ts, nlive);
         const char * Kt = smem + stage * MM_STAGE;
         const char * Vt = Kt + MM_KT;
 
