@@ -207,25 +207,11 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
         n_slots += ng;
     }
     const bool direct = L.size() == 1 && L[0].n_groups == 1;
-    // a single launch folds its slots in-kernel (last workgroups, two levels); several launches share the merge kernel
-    const bool kfold = !direct && L.size() == 1 && env_int("PA_HIP_DEC_FOLD", 0) != 0;
     if (!direct) {
         const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
         const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
         if (!ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") || !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
             return -1;
-    }
-    if (kfold) {   // level-1 slots (runs of 16 groups) and one counter per run plus one per head pair
-        const uint32_t n1 = (n_slots + 15) / 16;
-        const size_t go_b = (size_t) n1 * s->nkv * qr * s->hd * sizeof(float), gml_b = (size_t) n1 * s->nkv * qr * sizeof(float2);
-        if (!ensure(ws->go, ws->go_cap, go_b, "hipMalloc group slots") || !ensure(ws->gml, ws->gml_cap, gml_b, "hipMalloc group stats"))
-            return -1;
-        const size_t ctr_b = (size_t) (s->nkv / 2) * (n1 + 1) * sizeof(unsigned int);
-        if (ctr_b > ws->ctr_cap) {
-            if (!ensure(ws->ctr, ws->ctr_cap, std::max<size_t>(ctr_b, 4096), "hipMalloc counters") ||
-                !hip_ok(hipMemset(ws->ctr, 0, ws->ctr_cap), "hipMemset counters"))   // once per growth; kernels keep them zero
-                return -1;
-        }
     }
     const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
     ws->ev0 = ws->ev1 = nullptr;
@@ -247,10 +233,9 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
         a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_groups; a.chunk = tile;
         a.n_items = ln.n_groups * (s->nkv / 2);
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = 1; a.slot0 = ln.slot0;
-        a.qmode = s->qmode; a.fused = direct || kfold ? 1u : 0u; a.scale = s->scale;
+        a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale;
         a.s_mul = s->scale * 1.4426950408889634f;
         a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
-        a.counters = ws->ctr; a.go = ws->go; a.gml = ws->gml;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
         // the timing events (if any) at the start of the first and the end of the last decode kernel
         if (!hip_ok(launch_decode((int) s->fmt, a, grid, st, li == 0 ? ev0 : nullptr, li + 1 == L.size() ? ev1 : nullptr),
@@ -261,7 +246,7 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
         if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
         if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
     }
-    if (!direct && !kfold && !launch_fold(ws, n_slots, s->nkv, qr, s->rows, (int) s->hd, O, m, l, st)) return -1;
+    if (!direct && !launch_fold(ws, n_slots, s->nkv, qr, s->rows, (int) s->hd, O, m, l, st)) return -1;
     return 0;
 }
 
@@ -314,8 +299,7 @@ int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_page
         }
         a.pstart[ln.np] = acc;
         a.cstart[ln.np] = tacc;
-        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks;
-        a.chunk = env_int("PA_HIP_MMA_IL", 0) != 0 ? 0u : ln.tpc;  // 0: chunk c takes tiles c, c + n_chunks, ...
+        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.tpc;
         a.n_items = ln.n_chunks * units;
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale; a.s_mul = 1.4426950408889634f;

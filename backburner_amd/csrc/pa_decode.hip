@@ -161,34 +161,6 @@ __device__ __forceinline__ void dec_lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Split-K slot traffic between workgroups (possibly on different XCDs, whose L2 caches are not coherent): stores
-// written through and loads that bypass stale lines (agent-scope relaxed atomics: sc1), 8 bytes at a time, instead of
-// agent-scope fences, which write back and invalidate a whole L2.
-__device__ __forceinline__ void dec_st_wt(float * p, const pa_f4 & v) {
-    unsigned long long * q = (unsigned long long *) p;
-    const pa_u4 u = __builtin_bit_cast(pa_u4, v);
-    __hip_atomic_store(q, (unsigned long long) u.x | ((unsigned long long) u.y << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + 1, (unsigned long long) u.z | ((unsigned long long) u.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ pa_f4 dec_ld_wt(const float * p) {
-    const unsigned long long * q = (const unsigned long long *) p;
-    const unsigned long long a0 = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long a1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return __builtin_bit_cast(pa_f4, (pa_u4){(uint32_t) a0, (uint32_t) (a0 >> 32), (uint32_t) a1, (uint32_t) (a1 >> 32)});
-}
-__device__ __forceinline__ void dec_st_wt2(float2 * p, float2 v) {
-    __hip_atomic_store((unsigned long long *) p, __builtin_bit_cast(unsigned long long, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 dec_ld_wt2(const float2 * p) {
-    return __builtin_bit_cast(float2, __hip_atomic_load((const unsigned long long *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-// this wave's written-through stores complete (vmcnt 0), with a compiler ordering point on both sides
-__device__ __forceinline__ void dec_stores_done() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 template <int FMT>
 __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     using G = DecGeom<FMT>;
@@ -476,7 +448,7 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
         }
     }
     dec_wave_sync();
-    const bool direct = a.n_chunks == 1 && a.fused;
+    const bool direct = a.fused;                                     // one group holds the call: the final result
     const uint32_t r = n & 7;
     if (n < 8 && r < a.rows) {
         const float fo = arow[r], M = arow[8 + r], L = arow[16 + r];
@@ -484,71 +456,13 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
         for (int d = 0; d < DEC_ND; d++) {
             const pa_f4 v = O[d] * fo;
             if (direct) *(pa_f4 *) (a.O + ((size_t) h * a.rows + r) * DEC_HD + 16 * d + 4 * g) = v;
-            else if (a.fused) dec_st_wt(a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r) * DEC_HD + 16 * d + 4 * g, v);
             else *(pa_f4 *) (a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r) * DEC_HD + 16 * d + 4 * g) = v;
         }
         if (g == 0) {
             if (direct) { a.m[(size_t) h * a.rows + r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[(size_t) h * a.rows + r] = L; }
-            else if (a.fused) dec_st_wt2(a.pml + ((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r, make_float2(M, L));
             else a.pml[((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r] = make_float2(M, L);
         }
     }
-    if (direct || !a.fused) return;
-
-    // ---- in-kernel split-K fold (a single launch holding every group): the last workgroup of each run of DEC_FG
-    // groups of this head pair to finish folds their slots into a level-1 slot; the last of those folds the level-1
-    // slots into the final (O, m, l). Device-scope counters, one per run and one for the pair; no workgroup waits for
-    // another, and the last arrival resets its counter for the next call.
-    constexpr uint32_t DEC_FG = 16;
-    __shared__ uint32_t dec_last;
-    const uint32_t ng = a.n_chunks, n1 = (ng + DEC_FG - 1) / DEC_FG, g1 = c / DEC_FG;
-    unsigned int * ctr = a.counters + (size_t) pr * (n1 + 1);
-    // one wave folds its head: lane -> row lane / 8, dims 16 (lane % 8) .. +15; slot s of a source at rows
-    // ((s * nkv + h) * 8 + row) * 128
-    auto fold = [&](const float * srcO, const float2 * srcML, uint32_t s0, uint32_t ns, bool final, uint32_t dst_slot) {
-        const uint32_t rr = lane >> 3, d0 = 16 * (lane & 7);
-        if (rr >= a.rows) return;
-        float M = -INFINITY;
-        for (uint32_t s = s0; s < s0 + ns; s++) M = fmaxf(M, dec_ld_wt2(srcML + ((size_t) s * a.nkv + h) * DEC_QR + rr).x);
-        const float Ms = M == -INFINITY ? 0.0f : M;
-        pa_f4 acc[4] = {};
-        float L = 0.0f;
-        for (uint32_t s = s0; s < s0 + ns; s++) {
-            const size_t ro = ((size_t) s * a.nkv + h) * DEC_QR + rr;
-            const float2 ml = dec_ld_wt2(srcML + ro);
-            const float wgt = __builtin_amdgcn_exp2f(ml.x - Ms);     // -inf (an empty slot) -> 0
-            L += wgt * ml.y;
-            #pragma unroll
-            for (int j = 0; j < 4; j++) acc[j] += wgt * dec_ld_wt(srcO + ro * DEC_HD + d0 + 4 * j);
-        }
-        if (final) {
-            #pragma unroll
-            for (int j = 0; j < 4; j++) *(pa_f4 *) (a.O + ((size_t) h * a.rows + rr) * DEC_HD + d0 + 4 * j) = acc[j];
-            if ((lane & 7) == 0) { a.m[(size_t) h * a.rows + rr] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[(size_t) h * a.rows + rr] = L; }
-        } else {
-            const size_t ro = ((size_t) dst_slot * a.nkv + h) * DEC_QR + rr;
-            #pragma unroll
-            for (int j = 0; j < 4; j++) dec_st_wt(a.go + ro * DEC_HD + d0 + 4 * j, acc[j]);
-            if ((lane & 7) == 0) dec_st_wt2(a.gml + ro, make_float2(M, L));
-        }
-    };
-    // this workgroup's slots are written through (each wave waits for its stores), then counted
-    dec_stores_done();
-    __syncthreads();
-    const uint32_t cnt1 = min(DEC_FG, ng - DEC_FG * g1);
-    if (tid == 0) dec_last = __hip_atomic_fetch_add(&ctr[g1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == cnt1 - 1;
-    __syncthreads();
-    if (!dec_last) return;
-    fold(a.po, a.pml, a.slot0 + DEC_FG * g1, cnt1, n1 == 1, g1);
-    if (tid == 0) __hip_atomic_store(&ctr[g1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (n1 == 1) return;
-    dec_stores_done();
-    __syncthreads();
-    if (tid == 0) dec_last = __hip_atomic_fetch_add(&ctr[n1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n1 - 1;
-    __syncthreads();
-    if (!dec_last) return;
-    fold(a.go, a.gml, 0, n1, true, 0);
-    if (tid == 0) __hip_atomic_store(&ctr[n1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {

@@ -235,8 +235,9 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
 // PRE: PA_QMODE_GGML over quantized K. Q' then carries scale * log2 e inside its one fp16 rounding, and the QK
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
-template <int FMT, int NW, bool PRE, int PF>
+template <int FMT, int NW, bool PRE>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
+    constexpr int PF = 2;                                            // tiles whose raw bytes are in flight
     constexpr int NT = 64 * NW;
     constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
     static_assert(UPT * NT == 512, "NW must be 2, 4 or 8");
@@ -250,11 +251,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     if (local >= t8 || w >= a.n_items) return;
     const uint32_t rb = w % a.nrb, h = (w / a.nrb) % a.nkv, c = w / (a.nrb * a.nkv);
     const uint32_t T = a.cstart[a.n_pages];                          // 32-key tiles of the call
-    // this chunk's tiles t0 + k * ts, k < ntiles: consecutive (a.chunk per chunk), or with a.chunk = 0 interleaved,
-    // chunk c of NC taking tiles c, c + NC, ... (all workgroups stream through one narrow window of the cache)
-    const bool il = a.chunk == 0;
-    const uint32_t t0 = il ? c : c * a.chunk, ts = il ? a.n_chunks : 1u;
-    const uint32_t ntiles = il ? (T - c + ts - 1) / ts : min(t0 + a.chunk, T) - t0;   // >= 1: c < n_chunks <= T
+    const uint32_t t0 = c * a.chunk, ntiles = min(t0 + a.chunk, T) - t0;   // this chunk's tiles [t0, t0 + ntiles)
 
     const int tid = threadIdx.x, lane = tid % 64;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
@@ -268,7 +265,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     // ---- staging units of this thread: u = tid + NT*i -> tensor u >> 8 (= (wave + NW*i) >> 2, uniform), key
     // (u >> 3) & 31, block (u >> 1) & 3, half u & 1; rows past the page's end reload its last row (masked later)
     using F = MmFmt<FMT>;
-    MmRaw<FMT> R0[UPT], R1[UPT];                                     // tile t's raw bytes in R(t % PF)
+    MmRaw<FMT> R0[UPT], R1[UPT];                                     // tile t's raw bytes in R(t % 2)
     // buffer loads: the tile's first row of this head as the scalar base, its rows up to the page's end as the range.
     // Past the chunk's last tile (live false) the same loads go out with an empty range (no memory access, zeros), so
     // that every step issues the same batch and the wait before a tile's dequant covers its own batch only.
@@ -301,17 +298,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         }
     };
 
-    // ---- the first PF tiles' loads, then the query rows (B operand: lane (h2, n) holds row n, dims 16kk + 8h2 + t)
+    // ---- the first two tiles' loads, then the query rows (B operand: lane (h2, n) holds row n, dims 16kk + 8h2 + t)
     load_tile(R0, t0, true);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (PF == 2) load_tile(R1, t0 + ts, ntiles > 1);
+    load_tile(R1, t0 + 1, ntiles > 1);
     __builtin_amdgcn_sched_barrier(0);
     mm_h8 Qf[8];
     mm_prep_q<FMT, PRE>(a, h, row, rlive, h2, Qf);
 
-    // ---- prologue: tile t0 -> stage 0, the next tile (PF = 1), or the one after (PF = 2) in flight in R0
+    // ---- prologue: tile t0 -> stage 0, tile t0 + 2's loads in flight in R0 (t0 + 1's in R1)
     store_tile(R0, 0);
-    load_tile(R0, t0 + PF * ts, ntiles > PF);
+    load_tile(R0, t0 + PF, ntiles > PF);
     mm_lds_barrier();
 
     mm_f16 O[4];
@@ -327,15 +324,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     // one tile step; Rn holds tile t + 1's raw bytes
     auto step = [&](uint32_t t, MmRaw<FMT> (&Rn)[UPT]) {
         const int stage = t & 1;
-        const uint32_t tau = t0 + t * ts;
+        const uint32_t tau = t0 + t;
         cc.seek(a, tau);                                             // before any LDS operation of this step
         const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
         // the next tile's bytes -> the other stage (last read before the previous barrier; past the chunk's end the
         // stage is written and never read), then tile t + 1 + PF's loads into the registers just freed
         const bool nlive = t + 1 + PF < ntiles;
-        if (nlive) cl.seek(a, tau + (1 + PF) * ts);
+        if (nlive) cl.seek(a, tau + 1 + PF);
         store_tile(Rn, stage ^ 1);
-        load_tile(Rn, tau + (1 + PF) * ts, nlive);
+        load_tile(Rn, tau + 1 + PF, nlive);
         const char * Kt = smem + stage * MM_STAGE;
         const char * Vt = Kt + MM_KT;
 
@@ -405,35 +402,25 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             for (int mi = 0; mi < 2; mi++) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][mi], P[mi], O[db], 0, 0, 0);
         mm_lds_barrier();                                            // this stage is free; the next one is written
     };
-    if constexpr (PF == 1) {
-        for (uint32_t t = 0; t < ntiles; t++) step(t, R0);
-    } else {                                                         // tile t + 1 is in R((t + 1) % 2)
-        uint32_t t = 0;
-        for (; t + 2 <= ntiles; t += 2) {
-            step(t, R1);
-            step(t + 1, R0);
-        }
-        if (t < ntiles) step(t, R1);
+    uint32_t t = 0;                                                  // tile t + 1 is in R((t + 1) % 2)
+    for (; t + 2 <= ntiles; t += 2) {
+        step(t, R1);
+        step(t + 1, R0);
     }
+    if (t < ntiles) step(t, R1);
 
     mm_write_out(a, O, mref, mx, lsum, h, row, rlive, h2, c);
 }
 
-template <int FMT, bool PRE, int PF>
-static hipError_t launch_mma_pf(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+template <int FMT, bool PRE>
+static hipError_t launch_mma_fmt(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     switch (nw) {
-        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE, PF>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
-        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, PF>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, PF>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
+        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
+        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
-}
-
-template <int FMT, bool PRE>
-static hipError_t launch_mma_fmt(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    static const int pf = getenv("PA_HIP_MMA_PF") && atoi(getenv("PA_HIP_MMA_PF")) == 1 ? 1 : 2;
-    return pf == 1 ? launch_mma_pf<FMT, PRE, 1>(nw, a, grid, st, ev0, ev1) : launch_mma_pf<FMT, PRE, 2>(nw, a, grid, st, ev0, ev1);
 }
 
 hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
