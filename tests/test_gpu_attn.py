@@ -104,6 +104,36 @@ def test_split_invariance(ws, fmt):
         assert eo < 1e-3 and em < 1e-6 and el < 1e-5, (eo, em, el)
 
 
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0])
+@pytest.mark.parametrize("rows", [128, 512])
+def test_mma_split_invariance(ws, fmt, rows):
+    """The verify / prefill kernel over chunks of 1, 2, 3, 5 and 40 tiles (the two-tile register prefetch with its
+    empty-range loads past a chunk's end, uneven last chunks) and one chunk holding every tile (the result written
+    directly): each split is within the parity bar of the oracle, and splits agree with each other to the fp16
+    rounding of P, which the split moves (P is rounded relative to a different running max), in O and in l (the sum
+    of the same fp16 P that the PV product uses, 2^-11 per term at most), and on m to fp32 rounding."""
+    nkv, hd, nk = 2, 128, 5000                                # pages of 1500 keys: 157 tiles
+    K, V, Q, rs = case(fmt, nkv, rows, hd, nk, 91 + rows)
+    shape = bb.make_shape(nkv, rows, hd, fmt, rs=rs)
+    ref = orc.attn_ggml(orc.make_shape(nkv, rows, hd, fmt, orc.QMODE_GGML, rs=rs), Q, K, V, nk)
+    units = nkv * (2 if rows == 512 else 1)                   # KV heads x row blocks (256 rows per block at 512 rows)
+    outs = []
+    for want in (200, 100, 60, 35, 4, 1):                     # chunks of 1, 2, 3, 5, 40 and 157 tiles
+        env = {"PA_HIP_MMA_TARGET": str(want * units)}
+        print("mma split", env, flush=True)
+        os.environ.update(env)
+        try:
+            outs.append(bb.attn_host(shape, K, V, Q, page_keys=1500, ws=ws))
+        finally:
+            for k in env:
+                del os.environ[k]
+        eo, em, el = orc.rel_err(*outs[-1], *ref)
+        assert eo < TOL and em < TOL and el < TOL, (want, eo, em, el)
+    for O, m, l in outs[1:]:
+        eo, em, el = orc.rel_err(O, m, l, *outs[0])
+        assert eo < 1e-3 and em < 1e-6 and el < 2.0 ** -11, (eo, em, el)
+
+
 def test_bad_arguments(ws):
     with pytest.raises(bb.PaHipError, match="hd must be"):
         bb.attn_host(bb.make_shape(1, 8, 64, bb.FMT_Q8_0), np.zeros(68, np.uint8), np.zeros(68, np.uint8),
