@@ -123,9 +123,10 @@ def time_layers(bb, ws, lay: Layers, steps: int, warmup: int):
     return total_ms, kern, wall
 
 
-def time_layers_graph(bb, ws, lay: Layers, steps: int):
-    """The layer sequence captured once as a HIP graph (one pa_hip_attn per layer, its kernels in stream order), then
-    K timed replays: per-layer time without the host's per-launch overhead. Returns total ms, or None if the capture
+def time_layers_graph(bb, ws, lay: Layers, steps: int, reps: int = 1):
+    """The layer sequence, repeated reps times, captured once as a HIP graph (one pa_hip_attn per layer, its kernels in
+    stream order), then K timed replays: per-layer time without the host's per-launch overhead (a short sequence is
+    repeated so that one graph launch does not dominate). Returns total ms per reps sequences, or None if the capture
     failed."""
     syn = bb.synth()
     stream = syn.pa_synth_stream_new()
@@ -134,8 +135,9 @@ def time_layers_graph(bb, ws, lay: Layers, steps: int):
     syn.pa_synth_stream_sync(stream)
     if syn.pa_synth_capture_begin(stream) != 0:
         return None
-    for L in range(lay.n_layers):
-        ws.attn(lay.shape, lay.pages[L], lay.q[L].ptr, lay.O, lay.m, lay.l, stream)
+    for _ in range(reps):
+        for L in range(lay.n_layers):
+            ws.attn(lay.shape, lay.pages[L], lay.q[L].ptr, lay.O, lay.m, lay.l, stream)
     gx = syn.pa_synth_capture_end(stream)
     if not gx:
         return None
@@ -148,7 +150,7 @@ def time_layers_graph(bb, ws, lay: Layers, steps: int):
             raise RuntimeError("graph launch failed")
     syn.pa_synth_event_record(e1, stream)
     syn.pa_synth_stream_sync(stream)
-    total_ms = syn.pa_synth_event_ms(e0, e1)
+    total_ms = syn.pa_synth_event_ms(e0, e1) / reps
     syn.pa_synth_event_free(e0); syn.pa_synth_event_free(e1)
     syn.pa_synth_graph_free(gx)
     return total_ms
@@ -229,7 +231,7 @@ def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label):
     lay = Layers(bb, fmt, n_layers, n_keys, rows=rows)
     total_ms, kern, wall = time_layers(bb, ws, lay, steps, warmup)
     eager_us = total_ms * 1e3 / (steps * n_layers)
-    g_ms = time_layers_graph(bb, ws, lay, steps)
+    g_ms = time_layers_graph(bb, ws, lay, steps, reps=max(1, 64 // n_layers))
     if g_ms is not None:
         total_ms = g_ms
     per_layer_us = total_ms * 1e3 / (steps * n_layers)
