@@ -1,6 +1,8 @@
 // pa_abi.cpp - the C ABI of libpa_hip.so (declared in include/phone_attn_hip.h): the reference's sme_* entry points
 // (phone-attn.h:63-71) and the device-resident engine path. Host C++ over the HIP runtime; all compute runs in the HIP
-// kernels of pa_attn.hip / pa_accept.hip. There is no CPU fallback: without a gfx950 device every call fails loudly.
+// kernels (pa_decode.hip, pa_mma.hip, pa_attn.hip, pa_reply.hip, pa_ingest.hip, pa_accept.hip). There is no CPU
+// fallback: without a gfx950 device every call fails loudly. A workspace belongs to the device it was created on;
+// calls that use it expect that device to be current.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
