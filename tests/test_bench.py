@@ -1,0 +1,63 @@
+"""bench.py's output contract: one JSON line with the metric, the roofline of the decode kernel (traffic from the
+committed rocprofv3 counter summary) and the CPU baseline, and a refusal of more than one GPU. The CPU tests need no
+device; the GPU test runs a short bench (2 layers, 1 CPU-baseline layer) in a child process."""
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+ALG_BYTES = 2 * 131072 * 8 * 136 + 64 * 128 * 4 * 2 + 64 * 8    # K + V + Q + O, m, l of one 128k q8_0 decode layer
+
+
+def run_bench(*args, timeout=600):
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), *args], capture_output=True, text=True, timeout=timeout)
+    lines = [l for l in r.stdout.splitlines() if l.strip()]
+    return r.returncode, lines, r.stderr
+
+
+def test_more_than_one_gpu_is_refused():
+    rc, lines, _ = run_bench("--gpus", "2", timeout=120)
+    assert rc == 2 and len(lines) == 1
+    out = json.loads(lines[0])
+    assert out["n_gpus"] == 2 and "one GPU" in out["error"]
+
+
+def test_committed_traffic_summary():
+    """The decode kernel's HBM bytes per launch from the two PMC passes: at least the algorithmic bytes (K/V are read
+    once; FETCH_SIZE is scaled by the copy-kernel calibration), and not far above them."""
+    d = json.loads((ROOT / "profiles" / "decode128k_pmc.json").read_text())
+    assert d["alg_bytes_per_launch"] == ALG_BYTES
+    t = d["traffic_bytes_per_launch"]
+    assert ALG_BYTES <= t < 1.15 * ALG_BYTES
+    assert d["fetch_scale"] == pytest.approx(2.0, rel=0.01) and d["write_scale"] == pytest.approx(1.0, rel=0.01)
+    assert "dec_kernel" in (ROOT / "profiles" / "bench_all_kernels.md").read_text()
+
+
+@pytest.mark.gpu
+def test_bench_json_contract():
+    print("bench --steps 2 --warmup 1 --layers 2 --cpu-layers 1", flush=True)
+    rc, lines, err = run_bench("--steps", "2", "--warmup", "1", "--layers", "2", "--cpu-layers", "1")
+    assert rc == 0, err[-2000:]
+    assert len(lines) == 1, lines
+    out = json.loads(lines[0])
+    for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+              "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert k in out, k
+    assert out["n_gpus"] == 1 and out["steps"] == 2 and out["warmup"] == 1 and out["unit"] == "us/layer"
+    assert out["higher_is_better"] is False and out["vs_baseline"] is None and out["value"] > 0
+    assert out["ms_per_step"] == pytest.approx(out["value"] * 2 / 1e3, rel=1e-3)   # 2 layers per step
+    assert "workload" in out["config"] and out["config"]["seq_len"] == 131072
+    rf = out["roofline"]
+    assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["peak"] == 8000.0
+    assert rf["alg_bytes_per_launch"] == ALG_BYTES
+    assert rf["achieved"] == pytest.approx(ALG_BYTES / (rf["kernel_us_mean"] * 1e-6) / 1e9, rel=1e-3)
+    assert rf["frac"] == pytest.approx(rf["achieved"] / rf["peak"], rel=1e-3) and 0 < rf["frac"] < 1
+    assert rf["traffic"] >= ALG_BYTES
+    cb = out["cpu_baseline"]
+    assert cb["kind"] == "port" and cb["unit"] == "us/layer" and cb["cores"] >= 1 and cb["value"] > out["value"]
+    assert "orc_attn_ggml" in cb["sample"]
+    par = out["parity_vs_cpu"]
+    assert par["max_rel_O"] < 2e-3 and par["max_rel_m"] < 2e-3 and par["max_rel_l"] < 2e-3
