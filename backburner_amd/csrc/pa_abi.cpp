@@ -163,11 +163,13 @@ void reply_target(pa_hip_ws * ws, MergeArgs & ma) {
 }
 
 // merge the split-K slots of a call into (O, m, l); zero slots write (0, -inf, 0)
+// (decode and MMA slots: row-major, a row's slots contiguous)
 bool launch_fold(pa_hip_ws * ws, uint32_t n_slots, uint32_t nkv, uint32_t qr, uint32_t rows, int hd, float * O, float * m, float * l,
                  hipStream_t st) {
     MergeArgs ma;
     ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
     ma.n_slots = n_slots; ma.nkv = nkv; ma.qr = qr; ma.rows = rows;
+    ma.sst = 1; ma.rst = n_slots;
     reply_target(ws, ma);
     return hip_ok(launch_merge(hd, ma, st), "merge launch");
 }
@@ -234,7 +236,7 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
         a.cstart[ln.np] = tacc;
         a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_groups; a.chunk = tile;
         a.n_items = ln.n_groups * (s->nkv / 2);
-        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = 1; a.slot0 = ln.slot0;
+        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = 1; a.slot0 = ln.slot0; a.slots = n_slots;
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale;
         a.s_mul = s->scale * 1.4426950408889634f;
         a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
@@ -304,6 +306,7 @@ int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_page
         a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.tpc;
         a.n_items = ln.n_chunks * units;
         a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
+        a.slots = n_slots;
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale; a.s_mul = 1.4426950408889634f;
         a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
@@ -315,13 +318,7 @@ int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_page
         if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
         if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
     }
-    if (!direct) {
-        MergeArgs ma;
-        ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
-        ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
-        reply_target(ws, ma);
-        if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
-    }
+    if (!direct && !launch_fold(ws, n_slots, s->nkv, qr, s->rows, (int) s->hd, O, m, l, st)) return -1;
     return 0;
 }
 
@@ -415,6 +412,7 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         MergeArgs ma;
         ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
         ma.n_slots = 0; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        ma.sst = (uint64_t) s->nkv * qr; ma.rst = 1;
         reply_target(ws, ma);
         if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
     }
@@ -439,10 +437,11 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
         if (!hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch")) return -1;
     }
     if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;   // the attention kernel alone
-    if (!fused) {
+    if (!fused) {   // attn_kernel slots: slot-major
         MergeArgs ma;
         ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
         ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+        ma.sst = (uint64_t) s->nkv * qr; ma.rst = 1;
         reply_target(ws, ma);
         if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
     }

@@ -21,13 +21,14 @@ struct AttnArgs {
     uint32_t qr;                    // padded rows per KV head in the slots
     uint32_t nrb;                   // row blocks per KV head
     uint32_t slot0;                 // slot of chunk 0 of this launch
+    uint32_t slots;                 // decode / MMA kernels: the call's slot count (slots are row-major: [head, row][slot])
     uint32_t qmode;                 // PA_QMODE_GGML / PA_QMODE_F16
     uint32_t fused;                 // 1: this launch holds every chunk; the last workgroup per (head, row block) folds
     float scale;                    // softmax scale (PA_QMODE_F16 folds it into Q)
     float s_mul;                    // factor from the dot to base-2 logits (scale * log2 e, or log2 e)
     const float * q;                // [nkv][rows][hd] fp32
-    float * po;                     // slots [slot][nkv][qr][hd]
-    float2 * pml;                   // [slot][nkv][qr]: (max in base-2 units, sum)
+    float * po;                     // slots [nkv][qr][slots][hd] (decode, MMA) or [slot][nkv][qr][hd] (attn_kernel)
+    float2 * pml;                   // the same without hd: (max in base-2 units, sum)
     unsigned int * counters;        // [nkv][nrb][n_groups + 1] fold counters, zero between calls
     float * go;                     // first-level fold (group) slots [group][nkv][qr][hd]
     float2 * gml;                   // [group][nkv][qr]
@@ -39,6 +40,7 @@ struct MergeArgs {
     const float2 * pml;
     float * O, * m, * l;            // [nkv][rows][hd], [nkv][rows]
     uint32_t n_slots, nkv, qr, rows;
+    uint64_t sst = 0, rst = 0;      // slot s of output row h*qr + i at s*sst + (h*qr + i)*rst (rows of hd floats / one float2)
     uint16_t * Oh = nullptr;        // non-null: write the reply format instead of (O, m, l): Oh = f16(O / l) [nkv][rows][hd]
     float * lse = nullptr;          // and lse = m + log l [nkv][rows] (0 and -inf where l = 0)
 };

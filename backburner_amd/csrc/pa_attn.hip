@@ -539,10 +539,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     const uint32_t r = blockIdx.x;                   // output row = h*rows + i
     const uint32_t h = r / a.rows, i = r % a.rows;
     const int t = threadIdx.x, d4 = t % TPR, sg = t / TPR;
-    const size_t stride = (size_t) a.nkv * a.qr;     // rows between slots
-    const size_t pr = (size_t) h * a.qr + i;
+    const size_t pr = ((size_t) h * a.qr + i) * a.rst;              // slot s at s * a.sst + pr
     float M = -INFINITY;
-    for (uint32_t s = t; s < a.n_slots; s += 256) M = fmaxf(M, a.pml[s * stride + pr].x);
+    for (uint32_t s = t; s < a.n_slots; s += 256) M = fmaxf(M, a.pml[s * a.sst + pr].x);
     redm[t] = M;
     __syncthreads();
     for (int off = 128; off > 0; off >>= 1) {
@@ -554,10 +553,10 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
     pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
     float L = 0.0f;
     for (uint32_t s = sg; s < a.n_slots; s += SG) {
-        const float2 ml = a.pml[s * stride + pr];
+        const float2 ml = a.pml[s * a.sst + pr];
         const float w = __builtin_amdgcn_exp2f(ml.x - Ms);   // ml.x = -inf -> 0 (an empty slot)
         L += w * ml.y;
-        acc += w * *(const pa_f4 *) (a.po + (s * stride + pr) * HD + 4 * d4);
+        acc += w * *(const pa_f4 *) (a.po + (s * a.sst + pr) * HD + 4 * d4);
     }
     red[sg][d4] = acc;
     if (d4 == 0) redl[sg] = L;
@@ -588,15 +587,14 @@ __global__ __launch_bounds__(NT) void merge_wide_kernel(const MergeArgs a) {
     const uint32_t r = blockIdx.x / NQ, dq = blockIdx.x % NQ;   // output row h*rows + i, dims 32 dq .. +31
     const uint32_t h = r / a.rows, i = r % a.rows;
     const int t = threadIdx.x, lane = t % 64, wv = t / 64;
-    const size_t stride = (size_t) a.nkv * a.qr;
-    const size_t pr = (size_t) h * a.qr + i;
+    const size_t so = t * a.sst + ((size_t) h * a.qr + i) * a.rst;  // this thread's slot of the row
     const bool live = (uint32_t) t < a.n_slots;
     float2 ml = make_float2(-INFINITY, 0.0f);
     pa_f4 o[8];
     if (live) {
-        ml = a.pml[t * stride + pr];
+        ml = a.pml[so];
         #pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = *(const pa_f4 *) (a.po + (t * stride + pr) * HD + 32 * dq + 4 * j);
+        for (int j = 0; j < 8; j++) o[j] = *(const pa_f4 *) (a.po + so * HD + 32 * dq + 4 * j);
     } else {
         #pragma unroll
         for (int j = 0; j < 8; j++) o[j] = (pa_f4){0.f, 0.f, 0.f, 0.f};
@@ -657,15 +655,14 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const MergeArgs a) {
     const uint32_t r = blockIdx.x * RPW + t / TPR;                   // output row h*rows + i
     if (r >= a.nkv * a.rows) return;
     const uint32_t h = r / a.rows, i = r % a.rows;
-    const size_t stride = (size_t) a.nkv * a.qr;
-    const size_t pr = (size_t) h * a.qr + i;
+    const size_t pr = ((size_t) h * a.qr + i) * a.rst;              // slot s at s * a.sst + pr
     float2 ml[MS];
     pa_f4 o[MS];
     #pragma unroll
     for (int s = 0; s < MS; s++) {
         if ((uint32_t) s < a.n_slots) {
-            ml[s] = a.pml[s * stride + pr];
-            o[s] = *(const pa_f4 *) (a.po + (s * stride + pr) * HD + 4 * d4);
+            ml[s] = a.pml[s * a.sst + pr];
+            o[s] = *(const pa_f4 *) (a.po + (s * a.sst + pr) * HD + 4 * d4);
         } else {
             ml[s] = make_float2(-INFINITY, 0.0f);
             o[s] = (pa_f4){0.f, 0.f, 0.f, 0.f};

@@ -456,11 +456,11 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
         for (int d = 0; d < DEC_ND; d++) {
             const pa_f4 v = O[d] * fo;
             if (direct) *(pa_f4 *) (a.O + ((size_t) h * a.rows + r) * DEC_HD + 16 * d + 4 * g) = v;
-            else *(pa_f4 *) (a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r) * DEC_HD + 16 * d + 4 * g) = v;
+            else *(pa_f4 *) (a.po + (((size_t) h * a.qr + r) * a.slots + a.slot0 + c) * DEC_HD + 16 * d + 4 * g) = v;
         }
         if (g == 0) {
             if (direct) { a.m[(size_t) h * a.rows + r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[(size_t) h * a.rows + r] = L; }
-            else a.pml[((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + r] = make_float2(M, L);
+            else a.pml[((size_t) h * a.qr + r) * a.slots + a.slot0 + c] = make_float2(M, L);
         }
     }
 }

@@ -214,7 +214,7 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
     if (!rlive) return;
     const bool direct = a.n_chunks == 1 && a.fused;
     float * dst = direct ? a.O + ((size_t) h * a.rows + row) * MM_HD
-                         : a.po + (((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row) * MM_HD;
+                         : a.po + (((size_t) h * a.qr + row) * a.slots + a.slot0 + c) * MM_HD;
     #pragma unroll
     for (int db = 0; db < 4; db++)
         #pragma unroll
@@ -227,7 +227,7 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
             a.m[(size_t) h * a.rows + row] = mx == -INFINITY ? -INFINITY : mx * PA_LN2;
             a.l[(size_t) h * a.rows + row] = lt * f;
         } else {
-            a.pml[((size_t) (a.slot0 + c) * a.nkv + h) * a.qr + row] = make_float2(mx, lt * f);
+            a.pml[((size_t) h * a.qr + row) * a.slots + a.slot0 + c] = make_float2(mx, lt * f);
         }
     }
 }
