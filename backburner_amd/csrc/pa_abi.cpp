@@ -544,6 +544,17 @@ bool append_ok(const char * fn, const pa_hip_shape * s, void * const * kp, void 
     if (2ull * std::min(n, page_keys) * s->nkv * (s->hd / 32) >= (1ull << 31)) { set_err(f + ": segment too large"); return false; }
     return true;
 }
+
+// the pages that positions [pos0, pos0 + n) touch are al-byte aligned (the ingest kernels store 16- or 32-bit words)
+bool pages_aligned(const char * fn, void * const * kp, void * const * vp, uint32_t page_keys, uint32_t pos0, uint32_t n,
+                   uintptr_t al) {
+    for (uint64_t pi = pos0 / page_keys; n > 0 && pi <= (pos0 + (uint64_t) n - 1) / page_keys; pi++)
+        if (((uintptr_t) kp[pi] | (uintptr_t) vp[pi]) & (al - 1)) {
+            set_err(std::string(fn) + ": page " + std::to_string(pi) + " is not " + std::to_string(al) + "-byte aligned");
+            return false;
+        }
+    return true;
+}
 }  // namespace
 
 extern "C" int pa_hip_append_rows(const pa_hip_shape * s, void * const * k_pages, void * const * v_pages, int n_pages,
@@ -553,6 +564,7 @@ extern "C" int pa_hip_append_rows(const pa_hip_shape * s, void * const * k_pages
     const uint32_t srs = s ? (f16 ? s->nkv * s->hd * 2 : s->rs) : 0;
     if (!append_ok("pa_hip_append_rows", s, k_pages, v_pages, n_pages, page_keys, pos0, n)) return -1;
     if (n > 0 && (!K || !V)) { set_err("pa_hip_append_rows: null K/V"); return -1; }
+    if (f16 && !pages_aligned("pa_hip_append_rows", k_pages, v_pages, page_keys, pos0, n, 4)) return -1;
     hipStream_t st = (hipStream_t) stream;
     for (uint32_t done = 0; done < n;) {
         const uint32_t pos = pos0 + done, pi = pos / page_keys, off = pos % page_keys;
@@ -582,6 +594,9 @@ extern "C" int pa_hip_append_f32(const pa_hip_shape * s, void * const * k_pages,
     if (!append_ok("pa_hip_append_f32", s, k_pages, v_pages, n_pages, page_keys, pos0, n)) return -1;
     if (n > 0 && (!K || !V)) { set_err("pa_hip_append_f32: null K/V"); return -1; }
     if (((uintptr_t) K & 3) || ((uintptr_t) V & 3)) { set_err("pa_hip_append_f32: K/V must be 4-byte aligned"); return -1; }
+    const uint32_t al = s->fmt == PA_FMT_F16 ? 4 : 2;                // the stores are 32-bit (f16) or 16-bit words
+    if (s->rs % al || s->hb % al) { set_err("pa_hip_append_f32: rs and hb must be multiples of " + std::to_string(al)); return -1; }
+    if (!pages_aligned("pa_hip_append_f32", k_pages, v_pages, page_keys, pos0, n, al)) return -1;
     hipStream_t st = (hipStream_t) stream;
     for (uint32_t done = 0; done < n;) {
         const uint32_t pos = pos0 + done, pi = pos / page_keys, off = pos % page_keys;
@@ -602,6 +617,7 @@ extern "C" int pa_hip_append_f32(const pa_hip_shape * s, void * const * k_pages,
 extern "C" int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream) {
     if (fmt != PA_FMT_Q8_0 && fmt != PA_FMT_Q4_0) { set_err("pa_hip_quantize: fmt must be 1 or 2"); return -1; }
     if (n < 0 || n % 32 || (n > 0 && (!x || !y))) { set_err("pa_hip_quantize: n must be a multiple of 32"); return -1; }
+    if (((uintptr_t) x & 3) || ((uintptr_t) y & 1)) { set_err("pa_hip_quantize: x must be 4-byte and y 2-byte aligned"); return -1; }
     return hip_ok(launch_quantize(fmt, x, y, n, (hipStream_t) stream), "quantize launch") ? 0 : -1;
 }
 

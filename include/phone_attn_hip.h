@@ -146,19 +146,21 @@ int pa_hip_coattn_merge(const uint16_t * Oh, const float * lse, const float * O_
  * (k_pages / v_pages: host arrays of n_pages device pointers, from pa_hip_alloc_page). store_f16 with fmt q8_0 stores
  * each row as f16 values f16(d*q) instead (store_rows, phone-attn.h:305-319: stored row stride nkv*hd*2, head stride
  * hd*2; other formats are stored as received). K and V may be host memory for the plain copy; the f16 conversion
- * needs device-accessible sources (device memory or pinned host memory). Returns 0 once enqueued, -1 on a bad
- * argument (positions past the last page, a null page). */
+ * needs device-accessible sources (device memory or pinned host memory) and 4-byte aligned pages. Returns 0 once
+ * enqueued, -1 on a bad argument (positions past the last page, a null or misaligned page). */
 int pa_hip_append_rows(const pa_hip_shape * shape, void * const * k_pages, void * const * v_pages, int n_pages,
                        uint32_t page_keys, uint32_t pos0, const void * K, const void * V, uint32_t n, int store_f16,
                        void * stream);
 /* The sender's side of an APPEND, on the device: K and V fp32 [n][nkv][hd] (device pointers) quantized with the
  * library's ggml-semantics q8_0 / q4_0 quantizer (or converted to f16 for fmt f16) straight into the page rows at
- * positions pos0 .. pos0+n-1 (row format: the shape's rs and hb). No counterpart in the reference tree (the fork
- * quantizes K/V on the Mac before APPEND). Returns 0 or -1. */
+ * positions pos0 .. pos0+n-1 (row format: the shape's rs and hb, both even, multiples of 4 for f16; pages aligned
+ * alike; K and V 4-byte aligned). No counterpart in the reference tree (the fork quantizes K/V on the Mac before
+ * APPEND). Returns 0 or -1. */
 int pa_hip_append_f32(const pa_hip_shape * shape, void * const * k_pages, void * const * v_pages, int n_pages,
                       uint32_t page_keys, uint32_t pos0, const float * K, const float * V, uint32_t n, void * stream);
 /* q8_0 / q4_0 quantizer of the library (ggml quantize_row_q8_0_ref / q4_0_ref semantics; the q8_0 one prepares Q in
- * PA_QMODE_GGML): n fp32 values (multiple of 32) at x -> blocks at y, both device pointers. Returns 0 or -1. */
+ * PA_QMODE_GGML): n fp32 values (multiple of 32) at x (4-byte aligned) -> blocks at y (2-byte aligned), both device
+ * pointers. Returns 0 or -1. */
 int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream);
 
 #ifdef __cplusplus

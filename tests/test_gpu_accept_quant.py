@@ -87,6 +87,13 @@ def test_device_quantizer_bitexact(fmt):
     x[32:64] = np.arange(32, dtype=np.float32) - 16.0
     x[64:96] = 0.5
     x[96:128] = -3.0
+    x[128:160] = np.tile([2.0, -2.0], 16)                  # equal magnitudes, opposite signs: the first (+) sets q4_0's d
+    x[160:192] = np.tile([-2.0, 2.0], 16)                  # ... the first (-)
+    x[192:224] = -0.0                                      # an all -0 block: max stays +0, q4_0's d is -0
+    x[224:256] = rng.uniform(-1, 1, 32)
+    x[224 + 30], x[224 + 31] = -5.0, 5.0                   # the largest magnitude twice, at the block's end
+    x[256:288] = rng.uniform(-1, 1, 32)
+    x[256 + 17] = 7.0                                      # in the second half (the other 16 lanes' reduction)
     dx = bb.DeviceBuffer.from_array(x)
     hb = 34 if fmt == bb.FMT_Q8_0 else 18
     dy = bb.DeviceBuffer(nb * hb)

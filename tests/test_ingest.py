@@ -32,3 +32,25 @@ def test_rows_from_f32_layout_and_error_bound():
             x = X[:, h, :].reshape(-1)
             amax = np.abs(x.reshape(-1, 32)).max(axis=1).repeat(32)
             assert np.all(np.abs(deq - x) <= bound * (amax if fmt != orc.F16 else np.abs(x)) * 1.0001 + 1e-30)
+
+
+def test_ingest_rejects_misaligned_rows_pages_and_buffers():
+    """The ingest kernels store 16-bit (q8_0, q4_0) or 32-bit (f16) words: odd strides, misaligned pages and a misaligned
+    quantizer output are rejected on the host with a message, before any device call (the pointers here are never
+    dereferenced)."""
+    import pytest
+    import backburner_amd as bb
+    good = bb.Pages([0x10000], [0x20000], [0], [])
+    odd = bb.make_shape(2, 8, 128, bb.FMT_Q8_0, rs=2 * 136 + 1)
+    with pytest.raises(bb.PaHipError, match="multiples of 2"):
+        bb.append_f32(odd, good, 100, 0, 0x30000, 0x40000, 3)
+    f16 = bb.make_shape(2, 8, 128, bb.FMT_F16, rs=2 * 256 + 2)
+    with pytest.raises(bb.PaHipError, match="multiples of 4"):
+        bb.append_f32(f16, good, 100, 0, 0x30000, 0x40000, 3)
+    shape = bb.make_shape(2, 8, 128, bb.FMT_Q8_0)
+    with pytest.raises(bb.PaHipError, match="not 2-byte aligned"):
+        bb.append_f32(shape, bb.Pages([0x10001], [0x20000], [0], []), 100, 0, 0x30000, 0x40000, 3)
+    with pytest.raises(bb.PaHipError, match="not 4-byte aligned"):
+        bb.append_rows(shape, bb.Pages([0x10002], [0x20000], [0], []), 100, 0, 0x30000, 0x40000, 3, store_f16=True)
+    with pytest.raises(bb.PaHipError, match="2-byte aligned"):
+        bb.quantize_device(bb.FMT_Q8_0, 0x30000, 0x40001, 64)
