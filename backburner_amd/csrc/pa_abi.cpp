@@ -258,9 +258,14 @@ int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_p
 int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
              const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
     const int nw_env = env_int("PA_HIP_MMA_NW", 0);
-    const uint32_t nw = nw_env == 2 || nw_env == 4 || nw_env == 8 ? (uint32_t) nw_env : s->rows > 128 ? 8u : s->rows > 64 ? 4u : 2u;
+    // 4 waves up to 128 rows: the 2-wave kernel holds four staging units per thread, needs more than 256 registers and
+    // runs one wave per SIMD
+    const uint32_t nw = nw_env == 2 || nw_env == 4 || nw_env == 8 ? (uint32_t) nw_env : s->rows > 128 ? 8u : 4u;
     const uint32_t tile = 32;
     const uint32_t nrb = (s->rows + 32 * nw - 1) / (32 * nw), qr = nrb * 32 * nw;
+    // one row block with waves past the last row: those waves only stage (with several row blocks the full ones set
+    // the time, and the staging-only branch would slow them)
+    const bool skip = nrb == 1 && s->rows <= 32 * (nw - 1) && nw >= 4;
     const uint32_t units = s->nkv * nrb;
     // key chunks: about PA_HIP_MMA_TARGET workgroups in all; by default one round of resident ones (1 of 8 waves, 2 of
     // 4, 4 of 2 per CU, 256 CUs): a second, partial round costs more than the extra slots save
@@ -310,7 +315,7 @@ int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_page
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale; a.s_mul = 1.4426950408889634f;
         a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
-        if (!hip_ok(launch_mma((int) s->fmt, (int) nw, a, grid, st, li == 0 ? ev0 : nullptr, li + 1 == L.size() ? ev1 : nullptr),
+        if (!hip_ok(launch_mma((int) s->fmt, (int) nw, skip, a, grid, st, li == 0 ? ev0 : nullptr, li + 1 == L.size() ? ev1 : nullptr),
                     "mma launch"))
             return -1;
     }

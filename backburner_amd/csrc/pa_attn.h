@@ -49,7 +49,7 @@ hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st);
 hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
                          hipEvent_t ev1 = nullptr);
-hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
+hipError_t launch_mma(int fmt, int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
                       hipEvent_t ev1 = nullptr);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
 

@@ -235,7 +235,11 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
 // PRE: PA_QMODE_GGML over quantized K. Q' then carries scale * log2 e inside its one fp16 rounding, and the QK
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
-template <int FMT, int NW, bool PRE>
+// SKIP: a wave whose 32 rows are all past the call's rows only stages (its share of every tile's loads, dequant and LDS
+// stores, and the barriers). For calls with one row block narrower than 32 * NW rows; without SKIP the staging and the
+// matrix work of a step are one basic block, which the compiler interleaves (a branch between them costs 13-20 % on
+// full row blocks).
+template <int FMT, int NW, bool PRE, bool SKIP>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
     constexpr int PF = 2;                                            // tiles whose raw bytes are in flight
     constexpr int NT = 64 * NW;
@@ -258,6 +262,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     const int n = lane & 31, h2 = lane >> 5;
     const uint32_t row = rb * (32 * NW) + 32 * wave + n;             // this lane's query row (within the KV head)
     const bool rlive = row < a.rows;
+    const bool wlive = !SKIP || rb * (32 * NW) + 32 * wave < a.rows;    // uniform: the wave has a live row
 
     MmCursor cl, cc;                                                 // the next tile to load / to compute
     cl.init(a); cc.init(a);
@@ -321,18 +326,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     const mm_h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
 
     const int q4 = lane >> 4, s4 = lane & 15;
-    // one tile step; Rn holds tile t + 1's raw bytes
-    auto step = [&](uint32_t t, MmRaw<FMT> (&Rn)[UPT]) {
-        const int stage = t & 1;
-        const uint32_t tau = t0 + t;
-        cc.seek(a, tau);                                             // before any LDS operation of this step
-        const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
-        // the next tile's bytes -> the other stage (last read before the previous barrier; past the chunk's end the
-        // stage is written and never read), then tile t + 1 + PF's loads into the registers just freed
-        const bool nlive = t + 1 + PF < ntiles;
-        if (nlive) cl.seek(a, tau + 1 + PF);
-        store_tile(Rn, stage ^ 1);
-        load_tile(Rn, tau + 1 + PF, nlive);
+    // one tile's matrix work on LDS stage `stage` (nvalid keys)
+    auto compute = [&](int stage, int nvalid) {
         const char * Kt = smem + stage * MM_STAGE;
         const char * Vt = Kt + MM_KT;
 
@@ -400,6 +395,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         for (int db = 0; db < 4; db++)
             #pragma unroll
             for (int mi = 0; mi < 2; mi++) O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][mi], P[mi], O[db], 0, 0, 0);
+    };
+    // one tile step; Rn holds tile t + 1's raw bytes
+    auto step = [&](uint32_t t, MmRaw<FMT> (&Rn)[UPT]) {
+        const int stage = t & 1;
+        const uint32_t tau = t0 + t;
+        cc.seek(a, tau);                                             // before any LDS operation of this step
+        const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
+        // the next tile's bytes -> the other stage (last read before the previous barrier; past the chunk's end the
+        // stage is written and never read), then tile t + 1 + PF's loads into the registers just freed
+        const bool nlive = t + 1 + PF < ntiles;
+        if (nlive) cl.seek(a, tau + 1 + PF);
+        store_tile(Rn, stage ^ 1);
+        load_tile(Rn, tau + 1 + PF, nlive);
+        if (wlive) compute(stage, nvalid);
         mm_lds_barrier();                                            // this stage is free; the next one is written
     };
     uint32_t t = 0;                                                  // tile t + 1 is in R((t + 1) % 2)
@@ -413,21 +422,29 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
 }
 
 template <int FMT, bool PRE>
-static hipError_t launch_mma_fmt(int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+static hipError_t launch_mma_fmt(int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0,
+                                 hipEvent_t ev1) {
     switch (nw) {
-        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
-        case 4: hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 8: hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a); break;
+        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE, false>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
+        case 4:
+            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
+            else hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
+            break;
+        case 8:
+            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, true>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            else hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, false>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_mma(int fmt, int nw, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+hipError_t launch_mma(int fmt, int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0,
+                      hipEvent_t ev1) {
     const bool pre = a.qmode == 0;                                   // PA_QMODE_GGML (over quantized K)
-    if (fmt == 0) return launch_mma_fmt<0, false>(nw, a, grid, st, ev0, ev1);
-    if (fmt == 1) return pre ? launch_mma_fmt<1, true>(nw, a, grid, st, ev0, ev1) : launch_mma_fmt<1, false>(nw, a, grid, st, ev0, ev1);
-    if (fmt == 2) return pre ? launch_mma_fmt<2, true>(nw, a, grid, st, ev0, ev1) : launch_mma_fmt<2, false>(nw, a, grid, st, ev0, ev1);
+    if (fmt == 0) return launch_mma_fmt<0, false>(nw, skip, a, grid, st, ev0, ev1);
+    if (fmt == 1) return pre ? launch_mma_fmt<1, true>(nw, skip, a, grid, st, ev0, ev1) : launch_mma_fmt<1, false>(nw, skip, a, grid, st, ev0, ev1);
+    if (fmt == 2) return pre ? launch_mma_fmt<2, true>(nw, skip, a, grid, st, ev0, ev1) : launch_mma_fmt<2, false>(nw, skip, a, grid, st, ev0, ev1);
     return hipErrorInvalidValue;
 }
 

@@ -54,6 +54,14 @@ def test_parity_ggml(ws, fmt, rows, hd):
 
 
 @pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16])
+@pytest.mark.parametrize("rows", [9, 32, 33, 64, 100, 160, 224])
+def test_mma_row_blocks(ws, fmt, rows):
+    """One row block narrower than the workgroup's waves: 4 waves up to 128 rows (9-64 rows leave one to three waves
+    that only stage; 100 rows leave none), 8 waves above (160 and 224 rows leave three and one)."""
+    run_and_check(ws, fmt, 2, rows, 128, 1500, seed=300 + rows + fmt, page_keys=512)
+
+
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16])
 @pytest.mark.parametrize("rows", [8, 48])
 def test_parity_reference_rounding(ws, fmt, rows):
     run_and_check(ws, fmt, 4, rows, 256, 700, seed=7 + rows + fmt, qmode=bb.QMODE_F16, page_keys=256)
