@@ -61,6 +61,14 @@ def test_mma_row_blocks(ws, fmt, rows):
     run_and_check(ws, fmt, 2, rows, 128, 1500, seed=300 + rows + fmt, page_keys=512)
 
 
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0])
+@pytest.mark.parametrize("nkv,rows", [(1, 8), (3, 8), (3, 128)])
+def test_odd_kv_heads(ws, fmt, nkv, rows):
+    """An odd KV-head count has no head pairs for the decode kernel: decode goes to the matrix-core kernel (one live
+    wave per row block) and verify keeps its full row blocks; both over ragged pages."""
+    run_and_check(ws, fmt, nkv, rows, 128, 2100, seed=500 + 10 * nkv + rows + fmt, page_keys=1000)
+
+
 @pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16])
 @pytest.mark.parametrize("rows", [8, 48])
 def test_parity_reference_rounding(ws, fmt, rows):
