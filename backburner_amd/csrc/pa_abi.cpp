@@ -369,7 +369,10 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
 
     // split-K chunking per launch (pages go in groups of MAXP): about one workgroup per CU (PA_HIP_TARGET_WG), a chunk a
     // multiple of the key tile; a chunk may span pages
-    const int target = env_int("PA_HIP_TARGET_WG", cfg == CFG_DECODE ? (decode_variant() == 2 ? 256 : decode_variant() == 1 ? 1024 : 512) : 256);
+    // At head dim 256 the decode tile's 139 KB of LDS allow one workgroup per CU, so 256 is one round (8 rows x 4 KV
+    // heads x 65k q8_0 keys: 82 us, against 112 us at 1024); the 64-row workgroups measure best at 256 too.
+    const int target = env_int("PA_HIP_TARGET_WG", cfg == CFG_DECODE && s->hd != 256
+                                                       ? (decode_variant() == 2 ? 256 : decode_variant() == 1 ? 1024 : 512) : 256);
     const int forced_chunk = env_int("PA_HIP_CHUNK", 0);
     struct launch_t { int p0, np; uint32_t keys, chunk, n_chunks, slot0; };
     std::vector<launch_t> L;
