@@ -230,10 +230,10 @@ def read_traffic(name: str):
         return None
 
 
-def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label):
+def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label, nkv=8, hd=128):
     """Eager steps (per-kernel events), then the same layer sequence replayed as a HIP graph: the per-layer time is the
     graph's (no host launch cost), the eager one is kept beside it."""
-    lay = Layers(bb, fmt, n_layers, n_keys, rows=rows)
+    lay = Layers(bb, fmt, n_layers, n_keys, rows=rows, nkv=nkv, hd=hd)
     total_ms, kern, wall = time_layers(bb, ws, lay, steps, warmup)
     eager_us = total_ms * 1e3 / (steps * n_layers)
     g_ms = time_layers_graph(bb, ws, lay, steps, reps=max(1, 64 // n_layers))
@@ -284,14 +284,16 @@ def main():
 
     secondary = []
     if args.secondary:
-        for fmt, nl, nk, rows, label in (
-                (bb.FMT_Q8_0, 1, 4096, 8, "decode 4096 q8_0 keys (1 layer)"),
-                (bb.FMT_Q8_0, 64, 98304, 128, "verify 16 tokens, 98304 q8_0 keys, 64 layers"),
-                (bb.FMT_Q8_0, 64, 65536, 4096, "prefill 512 tokens, 65536 q8_0 keys, 64 distinct caches"),
-                (bb.FMT_Q4_0, 64, 143360, 8, "decode 143360 q4_0 keys, 64 layers"),
-                (bb.FMT_Q4_0, 64, 143360, 128, "verify 16 tokens, 143360 q4_0 keys, 64 layers")):
+        for fmt, nl, nk, rows, nkv, hd, label in (
+                (bb.FMT_Q8_0, 1, 4096, 8, 8, 128, "decode 4096 q8_0 keys (1 layer)"),
+                (bb.FMT_Q8_0, 64, 98304, 128, 8, 128, "verify 16 tokens, 98304 q8_0 keys, 64 layers"),
+                (bb.FMT_Q8_0, 64, 65536, 4096, 8, 128, "prefill 512 tokens, 65536 q8_0 keys, 64 distinct caches"),
+                (bb.FMT_Q4_0, 64, 143360, 8, 8, 128, "decode 143360 q4_0 keys, 64 layers"),
+                (bb.FMT_Q4_0, 64, 143360, 128, 8, 128, "verify 16 tokens, 143360 q4_0 keys, 64 layers"),
+                (bb.FMT_Q8_0, 16, 65536, 48, 4, 256,
+                 "the reference's own shape: 48 rows x 4 KV heads, head dim 256, 65536 q8_0 keys, 16 layers")):
             st = max(2, min(args.steps, 10)) if rows > 8 else args.steps
-            l2, r2, _, _ = run_config(bb, ws, fmt, nl, nk, rows, st, 1, label)
+            l2, r2, _, _ = run_config(bb, ws, fmt, nl, nk, rows, st, 1, label, nkv=nkv, hd=hd)
             l2.close()
             log("secondary", json.dumps(r2))
             secondary.append(r2)
