@@ -575,30 +575,28 @@ __global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
 }
 
 // Many slots (split-K decode up to 256, verify up to 64): one workgroup of NT threads (256, or one wave for at most 64
-// slots) per (row, 32 dims), one thread per slot, so that every load of the fold is issued at once (one memory
-// latency, not one per slot): thread t reads slot t's (max, sum) and its 32 dims, the workgroup reduces the max and
-// the weighted sums through LDS.
+// slots) per (row, 32 dims), every load of the fold issued at once (one memory latency, not one per slot). Lane l of
+// wave v reads dims 4 (l % 8) .. +3 of slots 64 v + l / 8 + 8 j (j < 8), so that eight lanes read one slot's 128 bytes
+// and a load instruction touches eight whole lines; thread t also reads slot t's (max, sum). The weights reach the
+// lanes that hold a slot's dims by a shuffle, the dims' sums by xor-shuffles over the eight-lane groups, then across
+// waves through LDS.
 template <int HD, int NT>
 __global__ __launch_bounds__(NT) void merge_wide_kernel(const MergeArgs a) {
-    constexpr int NQ = HD / 32, NWV = NT / 64, NSEG = NT / 32;
-    __shared__ float sO[NT][33];                    // slot x dim (padded: column sums read conflict-free)
-    __shared__ float sP[NSEG][32];
+    constexpr int NQ = HD / 32, NWV = NT / 64;
     __shared__ float sM[NWV], sL[NWV];
+    __shared__ pa_f4 sA[NWV][8];
     const uint32_t r = blockIdx.x / NQ, dq = blockIdx.x % NQ;   // output row h*rows + i, dims 32 dq .. +31
     const uint32_t h = r / a.rows, i = r % a.rows;
     const int t = threadIdx.x, lane = t % 64, wv = t / 64;
-    const size_t so = t * a.sst + ((size_t) h * a.qr + i) * a.rst;  // this thread's slot of the row
-    const bool live = (uint32_t) t < a.n_slots;
-    float2 ml = make_float2(-INFINITY, 0.0f);
+    const size_t pr = ((size_t) h * a.qr + i) * a.rst;              // slot s of the row at s * a.sst + pr
     pa_f4 o[8];
-    if (live) {
-        ml = a.pml[so];
-        #pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = *(const pa_f4 *) (a.po + so * HD + 32 * dq + 4 * j);
-    } else {
-        #pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = (pa_f4){0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t s = 64 * wv + lane / 8 + 8 * j;
+        o[j] = s < a.n_slots ? *(const pa_f4 *) (a.po + (s * a.sst + pr) * HD + 32 * dq + 4 * (lane % 8))
+                             : (pa_f4){0.f, 0.f, 0.f, 0.f};
     }
+    const float2 ml = (uint32_t) t < a.n_slots ? a.pml[t * a.sst + pr] : make_float2(-INFINITY, 0.0f);
     float M = ml.x;
     #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
@@ -613,36 +611,36 @@ __global__ __launch_bounds__(NT) void merge_wide_kernel(const MergeArgs a) {
     float L = w * ml.y;
     #pragma unroll
     for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
-    if (lane == 0) sL[wv] = L;
+    pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
     #pragma unroll
-    for (int j = 0; j < 8; j++)
+    for (int j = 0; j < 8; j++) acc += __shfl(w, lane / 8 + 8 * j) * o[j];   // slot 64 wv + l / 8 + 8 j is this wave's lane l / 8 + 8 j
+    #pragma unroll
+    for (int off = 8; off < 64; off <<= 1)
         #pragma unroll
-        for (int k = 0; k < 4; k++) sO[t][4 * j + k] = w * o[j][k];
-    __syncthreads();
-    {                                                                // column sums over NSEG segments of 32 slots
-        const int c = t % 32, seg = t / 32;
-        float acc = 0.0f;
+        for (int k = 0; k < 4; k++) acc[k] += __shfl_xor(acc[k], off);
+    if constexpr (NWV > 1) {
+        if (lane < 8) sA[wv][lane] = acc;
+        if (lane == 0) sL[wv] = L;
+        __syncthreads();
+        if (wv != 0 || lane >= 8) return;
+        acc = sA[0][lane];
+        L = sL[0];
         #pragma unroll
-        for (int q = 0; q < 32; q++) acc += sO[32 * seg + q][c];
-        sP[seg][c] = acc;
+        for (int k = 1; k < NWV; k++) { acc += sA[k][lane]; L += sL[k]; }
+    } else if (lane >= 8) {
+        return;
     }
-    __syncthreads();
-    if (t < 32) {
-        float acc = 0.0f;
-        #pragma unroll
-        for (int seg = 0; seg < NSEG; seg++) acc += sP[seg][t];
-        float Lt = 0.0f;
-        #pragma unroll
-        for (int k = 0; k < NWV; k++) Lt += sL[k];
-        if (a.Oh) {
-            merge_write_reply<1>(a, (size_t) r * HD + 32 * dq + t, &acc, M, Lt, r, dq == 0 && t == 0);
-            return;
-        }
-        a.O[(size_t) r * HD + 32 * dq + t] = acc;
-        if (dq == 0 && t == 0) {
-            a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2;
-            a.l[r] = Lt;
-        }
+    // lanes 0-7 of wave 0: dims 32 dq + 4 lane .. +3
+    const size_t off = (size_t) r * HD + 32 * dq + 4 * lane;
+    if (a.Oh) {
+        const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+        merge_write_reply<4>(a, off, v, M, L, r, dq == 0 && lane == 0);
+        return;
+    }
+    *(pa_f4 *) (a.O + off) = acc;
+    if (dq == 0 && lane == 0) {
+        a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2;
+        a.l[r] = L;
     }
 }
 
