@@ -236,9 +236,9 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
 // SKIP: a wave whose 32 rows are all past the call's rows only stages (its share of every tile's loads, dequant and LDS
-// stores, and the barriers). For calls with one row block narrower than 32 * NW rows; without SKIP the staging and the
-// matrix work of a step are one basic block, which the compiler interleaves (a branch between them costs 13-20 % on
-// full row blocks).
+// stores, and the barriers). For calls with one row block narrower than 32 * NW rows. Without SKIP there is no branch
+// there: one costs 13-20 % on full row blocks, as it separates the next tile's loads from the QK MFMAs, which the
+// compiler otherwise schedules in one basic block.
 template <int FMT, int NW, bool PRE, bool SKIP>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
     constexpr int PF = 2;                                            // tiles whose raw bytes are in flight
