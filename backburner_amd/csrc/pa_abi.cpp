@@ -466,7 +466,7 @@ extern "C" int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, i
     if (vocab < 1 || vocab > 0x7fffffffLL) { set_err("pa_hip_accept: vocab must be 1..2^31-1"); return -1; }
     if ((vocab & 3) == 0 && ((uintptr_t) logits & 15)) { set_err("pa_hip_accept: logits must be 16-byte aligned"); return -1; }
     // about 256 workgroups in total, each slice at least 4096 values
-    const int splits = (int) ((vocab + 4095) / 4096);                // 4096 values per workgroup (the kernel's slice)
+    const int splits = (int) ((vocab + ACCEPT_SEG - 1) / ACCEPT_SEG);   // ACCEPT_SEG values per workgroup (the kernel's slice)
     const size_t need = (size_t) n_rows * splits * sizeof(unsigned long long);
     if (!ensure(ws->apart, ws->apart_cap, need, "hipMalloc accept partials")) return -1;
     AcceptArgs a;

@@ -4,9 +4,9 @@
 // block verification, serve.sh:300-302). Semantics: a_i = argmax_j logits[i][j] with the lowest index on ties (numpy's
 // rule, which also makes the first NaN win); k = the longest prefix with a_i == draft_i (i < n_rows-1); bonus = a_k.
 //
-// Layout: n_rows x splits workgroups; workgroup (row, sp) scans values [4096 sp, 4096 sp + 4096) of its row, every
-// thread issuing all its loads at once (four 16-byte loads, or sixteen scalar ones when the vocab is not a multiple
-// of 4), and reduces a 64-bit key (orderable value << 32 | ~index) so that one unsigned max picks the largest value
+// Layout: n_rows x splits workgroups; workgroup (row, sp) scans values [S sp, S sp + S) of its row (S = ACCEPT_SEG),
+// every thread issuing all its loads at once (S / 1024 16-byte loads, or S / 256 scalar ones when the vocab is not a
+// multiple of 4), and reduces a 64-bit key (orderable value << 32 | ~index) so that one unsigned max picks the largest value
 // and, among equal values, the lowest index. Each workgroup publishes its key with a write-through store and waits for
 // it to complete before it counts itself done on a device-scope counter; the last one reads the keys with
 // write-through loads, folds them per row and computes (k, bonus). No cache write-back or invalidate is needed: the
@@ -27,7 +27,6 @@ __device__ __forceinline__ unsigned long long accept_key(float x, uint32_t idx) 
     return ((unsigned long long) k << 32) | (unsigned long long) (0xffffffffu - idx);
 }
 
-constexpr int64_t ACCEPT_SEG = 4096;                                 // values per workgroup
 
 __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
 
@@ -40,14 +39,15 @@ __global__ __launch_bounds__(256) void accept_kernel(const AcceptArgs a) {
     unsigned long long best = 0;
     const int t = threadIdx.x;
     if ((a.vocab & 3) == 0) {                                        // j < j1 implies j + 3 < vocab
-        pa_f4 v[4];
+        constexpr int NU = ACCEPT_SEG / 1024;
+        pa_f4 v[NU];
         #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < NU; u++) {
             const int64_t j = j0 + 4 * t + 1024 * u;
             v[u] = j < j1 ? *(const pa_f4 *) (x + j) : (pa_f4){0.f, 0.f, 0.f, 0.f};
         }
         #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < NU; u++) {
             const int64_t j = j0 + 4 * t + 1024 * u;
             if (j < j1) {
                 #pragma unroll
@@ -55,14 +55,15 @@ __global__ __launch_bounds__(256) void accept_kernel(const AcceptArgs a) {
             }
         }
     } else {
-        float v[16];
+        constexpr int NU = ACCEPT_SEG / 256;
+        float v[NU];
         #pragma unroll
-        for (int u = 0; u < 16; u++) {
+        for (int u = 0; u < NU; u++) {
             const int64_t j = j0 + t + 256 * u;
             v[u] = j < j1 ? x[j] : 0.0f;
         }
         #pragma unroll
-        for (int u = 0; u < 16; u++) {
+        for (int u = 0; u < NU; u++) {
             const int64_t j = j0 + t + 256 * u;
             if (j < j1) best = umax64(best, accept_key(v[u], (uint32_t) j));
         }

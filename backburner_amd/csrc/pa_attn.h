@@ -71,6 +71,13 @@ hipError_t launch_coattn(int hd, const uint16_t * Oh, const float * lse, const f
 void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb);
 int decode_variant();
 
+#ifndef PA_ACCEPT_SEG
+#define PA_ACCEPT_SEG 16384
+#endif
+// logits per acceptance workgroup (a multiple of 1024). [17][151936] fp32: 7.2 us at 16384 (170 workgroups), 8.3 at
+// 8192, 8.8 at 32768, 12.0 at 4096 - fewer, fuller workgroups, and fewer keys for the last one to fold
+constexpr int ACCEPT_SEG = PA_ACCEPT_SEG;
+
 struct AcceptArgs {
     const float * logits;
     const int32_t * draft;
