@@ -87,6 +87,8 @@ def lib() -> C.CDLL:
     L.pa_hip_attn.argtypes = [vp, C.POINTER(Shape), C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_uint32), C.c_int, vp, vp, vp, vp, vp]
     L.pa_hip_accept.restype = C.c_int
     L.pa_hip_accept.argtypes = [vp, vp, C.c_int, C.c_int64, vp, vp, vp]
+    L.pa_hip_ws_set_split.restype = C.c_int
+    L.pa_hip_ws_set_split.argtypes = [vp, C.c_int, C.c_int]
     L.pa_hip_ws_time_next.restype = C.c_int
     L.pa_hip_ws_time_next.argtypes = [vp, vp, vp]
     L.pa_hip_quantize.restype = C.c_int
@@ -298,6 +300,10 @@ class Workspace:
         vp = (C.c_void_p * max(n, 1))(*pages.v)
         nk = (C.c_uint32 * max(n, 1))(*pages.nkeys)
         _check(lib().pa_hip_attn_reply(self.ptr, C.byref(shape), kp, vp, nk, n, Q, Oh, lse, stream), "pa_hip_attn_reply")
+
+    def set_split(self, decode_groups: int = 0, mma_workgroups: int = 0) -> None:
+        """pa_hip_ws_set_split: force the split-K geometry of this workspace's calls (0 = default)."""
+        _check(lib().pa_hip_ws_set_split(self.ptr, decode_groups, mma_workgroups), "pa_hip_ws_set_split")
 
     def time_next(self, ev_start, ev_end) -> None:
         """Record ev_start / ev_end around the attention kernel of the next attn() call."""

@@ -60,29 +60,20 @@ uint32_t head_bytes(int fmt, int hd) {
     return fmt == PA_FMT_Q8_0 ? (uint32_t) (hd / 32 * 34) : fmt == PA_FMT_Q4_0 ? (uint32_t) (hd / 32 * 18) : (uint32_t) (hd * 2);
 }
 
-template <typename T> bool ensure(T *& p, size_t & cap, size_t need_bytes, const char * what) {
-    if (need_bytes <= cap && p) return true;
-    if (p) { (void) hipDeviceSynchronize(); (void) hipFree(p); p = nullptr; cap = 0; }
-    const size_t sz = std::max<size_t>(need_bytes, 256);
-    if (!hip_ok(hipMalloc((void **) &p, sz), what)) return false;
-    cap = sz;
-    return true;
-}
-
-int env_int(const char * name, int def) { const char * e = getenv(name); return e ? atoi(e) : def; }
-
 }  // namespace
 
 // ---------------------------------------------------------------- the workspace
 struct pa_hip_ws {
     int device = 0;
     float * po = nullptr; size_t po_cap = 0;
-    unsigned int * ctr = nullptr; size_t ctr_cap = 0;
     float2 * pml = nullptr; size_t pml_cap = 0;
-    float * go = nullptr; size_t go_cap = 0;
-    float2 * gml = nullptr; size_t gml_cap = 0;
     unsigned long long * apart = nullptr; size_t apart_cap = 0;
     unsigned int * acount = nullptr;
+    // buffers replaced by a larger one: a graph captured earlier may still name them, so they live as long as the
+    // workspace (growth at least doubles a buffer, so they hold less than the live ones)
+    std::vector<void *> retired;
+    // split-K geometry overrides (pa_hip_ws_set_split); 0 = the default geometry
+    int dec_groups = 0, mma_workgroups = 0;
     // the sme_* compatibility path: its own stream and staging buffers
     hipStream_t stream = nullptr;
     uint8_t * dk = nullptr; size_t dk_cap = 0;
@@ -91,13 +82,40 @@ struct pa_hip_ws {
     float * dout = nullptr; size_t dout_cap = 0;
     // measurement hook (pa_hip_ws_time_next)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    // pa_hip_attn_reply: (O, m, l) staging, and the reply target the split-K merge writes directly when the call has one
+    // pa_hip_attn_reply: (O, m, l) staging
     float * ro = nullptr; size_t ro_cap = 0;
     float * rml = nullptr; size_t rml_cap = 0;
-    uint16_t * reply_oh = nullptr;
-    float * reply_lse = nullptr;
-    bool reply_done = false;
 };
+
+namespace {
+
+// A device buffer of the workspace with room for need_bytes. A larger one replaces it when needed: keep_old retires the
+// old one (freed with the workspace: the engine path's buffers, which a captured graph may hold), otherwise it is freed
+// once the stream is idle (the synchronous sme_* staging). Growth while `st` is being captured is refused: hipMalloc
+// would end the capture, and the graph would hold a buffer the next growth replaces.
+template <typename T>
+bool ensure(pa_hip_ws * ws, T *& p, size_t & cap, size_t need_bytes, hipStream_t st, bool keep_old, const char * what) {
+    if (need_bytes <= cap && p) return true;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        set_err(std::string(what) + ": the workspace must grow (" + std::to_string(need_bytes) +
+                " bytes) inside a stream capture; make one eager call of the largest shape before capturing");
+        return false;
+    }
+    (void) hipGetLastError();
+    const size_t sz = std::max<size_t>({need_bytes, 2 * cap, 256});
+    T * np = nullptr;
+    if (!hip_ok(hipMalloc((void **) &np, sz), what)) return false;
+    if (p) {
+        if (keep_old) ws->retired.push_back((void *) p);
+        else { (void) hipStreamSynchronize(st); (void) hipFree(p); }
+    }
+    p = np;
+    cap = sz;
+    return true;
+}
+
+}  // namespace
 
 extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
     if (!device_usable()) { set_err("pa_hip_ws_new: " + g_dev_why); return nullptr; }
@@ -115,8 +133,9 @@ extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
 extern "C" void pa_hip_ws_destroy(pa_hip_ws * w) {
     if (!w) return;
     (void) hipDeviceSynchronize();
-    hipFree(w->ctr); hipFree(w->go); hipFree(w->gml); hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
+    hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
     hipFree(w->dk); hipFree(w->dv); hipFree(w->dq); hipFree(w->dout); hipFree(w->ro); hipFree(w->rml);
+    for (void * p : w->retired) hipFree(p);
     if (w->stream) hipStreamDestroy(w->stream);
     delete w;
 }
@@ -126,6 +145,13 @@ extern "C" const char * pa_hip_last_error(void) { return g_err.c_str(); }
 extern "C" int pa_hip_ws_time_next(pa_hip_ws * ws, void * ev_start, void * ev_end) {
     if (!ws) { set_err("pa_hip_ws_time_next: null workspace"); return -1; }
     ws->ev0 = (hipEvent_t) ev_start; ws->ev1 = (hipEvent_t) ev_end;
+    return 0;
+}
+
+extern "C" int pa_hip_ws_set_split(pa_hip_ws * ws, int decode_groups, int mma_workgroups) {
+    if (!ws || decode_groups < 0 || mma_workgroups < 0) { set_err("pa_hip_ws_set_split: null workspace or negative count"); return -1; }
+    ws->dec_groups = decode_groups;
+    ws->mma_workgroups = mma_workgroups;
     return 0;
 }
 
@@ -146,317 +172,351 @@ extern "C" void pa_hip_free_page(void * k, void * v) {
 // ---------------------------------------------------------------- the engine path
 namespace {
 
-int pick_cfg(uint32_t rows, uint32_t hd) {
-    const int forced = env_int("PA_HIP_CFG", -1);
-    if (forced >= 0 && forced <= CFG_PREFILL) return forced;
-    if (rows <= 16) return CFG_DECODE;
-    if (rows <= 64 || hd == 256) return CFG_MID;
-    if (rows <= 128) return CFG_VERIFY;
-    return CFG_PREFILL;
+constexpr int DEC_TARGET_WG = 1024;   // decode workgroups per launch: four of two waves per CU
+constexpr int GEN_TARGET_WG = 256;    // head dim 256 kernel: one round of resident workgroups
+
+// One call of the engine path: where its split-K slots go, its geometry overrides, its timing events and, for
+// pa_hip_attn_reply, the reply target the merge writes instead of (O, m, l).
+struct Call {
+    pa_hip_ws * ws = nullptr;         // slots in this workspace's buffers (grown on demand) ...
+    char * fixed = nullptr;           // ... or in a fixed device array of `cap` bytes (nothing allocated)
+    size_t cap = 0;
+    int dec_groups = 0, mma_workgroups = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    uint16_t * reply_oh = nullptr;
+    float * reply_lse = nullptr;
+    bool reply_done = false;
+    float * po = nullptr;
+    float2 * pml = nullptr;
+
+    // slot rows (one row = hd floats of O and a (max, sum) pair) that a fixed array holds; unlimited for a workspace
+    uint64_t max_rows(uint32_t hd) const {
+        return fixed ? (cap - 256) / ((uint64_t) hd * sizeof(float) + sizeof(float2)) : ~0ull;
+    }
+    bool slots(uint64_t rows, uint32_t hd, hipStream_t st) {
+        const size_t po_b = std::max<uint64_t>(rows, 1) * hd * sizeof(float);
+        const size_t pml_b = std::max<uint64_t>(rows, 1) * sizeof(float2);
+        if (fixed) {
+            if (rows > max_rows(hd)) {
+                set_err("the call's split-K slots (" + std::to_string(po_b + pml_b) + " bytes) exceed the fixed scratch (" +
+                        std::to_string(cap) + " bytes)");
+                return false;
+            }
+            po = (float *) fixed;
+            pml = (float2 *) (fixed + (po_b + 255) / 256 * 256);
+            return true;
+        }
+        if (!ensure(ws, ws->po, ws->po_cap, po_b, st, true, "hipMalloc partials") ||
+            !ensure(ws, ws->pml, ws->pml_cap, pml_b, st, true, "hipMalloc partial stats"))
+            return false;
+        po = ws->po;
+        pml = ws->pml;
+        return true;
+    }
+    // the merge of the call's slots: the reply format when asked for, else (O, m, l)
+    bool merge(MergeArgs & ma, int hd, hipStream_t st) {
+        if (reply_oh) { ma.Oh = reply_oh; ma.lse = reply_lse; reply_done = true; }
+        return hip_ok(launch_merge(hd, ma, st), "merge launch");
+    }
+};
+
+// The launches of a call: pages in groups of MAXP (their pointers travel in the kernel arguments), calling
+// f(first page, pages, 32-key tiles, keys) for each group that holds keys.
+template <class F> void for_launches(const uint32_t * nkeys, int n_pages, F f) {
+    for (int p0 = 0; p0 < n_pages; p0 += MAXP) {
+        const int np = std::min(MAXP, n_pages - p0);
+        uint64_t tiles = 0, keys = 0;
+        for (int i = 0; i < np; i++) { tiles += (nkeys[p0 + i] + 31) / 32; keys += nkeys[p0 + i]; }
+        if (tiles) f(p0, np, tiles, keys);
+    }
 }
 
-// pa_hip_attn_reply: the merge writes the reply format itself (the caller's (O, m, l) then stay unwritten)
-void reply_target(pa_hip_ws * ws, MergeArgs & ma) {
-    if (!ws->reply_oh) return;
-    ma.Oh = ws->reply_oh; ma.lse = ws->reply_lse;
-    ws->reply_done = true;
+// the page table of one launch: page bases, key prefix and 32-key tile prefix
+void page_table(AttnArgs & a, const void * const * k_pages, const void * const * v_pages, const uint32_t * nkeys, int p0, int np) {
+    uint32_t acc = 0, tacc = 0;
+    for (int i = 0; i < np; i++) {
+        a.kp[i] = (const uint8_t *) k_pages[p0 + i];
+        a.vp[i] = (const uint8_t *) v_pages[p0 + i];
+        a.pstart[i] = acc;
+        a.cstart[i] = tacc;
+        acc += nkeys[p0 + i];
+        tacc += (nkeys[p0 + i] + 31) / 32;
+    }
+    a.pstart[np] = acc;
+    a.cstart[np] = tacc;
+    a.n_pages = (uint32_t) np;
 }
 
-// merge the split-K slots of a call into (O, m, l); zero slots write (0, -inf, 0)
-// (decode and MMA slots: row-major, a row's slots contiguous)
-bool launch_fold(pa_hip_ws * ws, uint32_t n_slots, uint32_t nkv, uint32_t qr, uint32_t rows, int hd, float * O, float * m, float * l,
-                 hipStream_t st) {
-    MergeArgs ma;
-    ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
-    ma.n_slots = n_slots; ma.nkv = nkv; ma.qr = qr; ma.rows = rows;
-    ma.sst = 1; ma.rst = n_slots;
-    reply_target(ws, ma);
-    return hip_ok(launch_merge(hd, ma, st), "merge launch");
+// With a fixed slot array: the most chunks per launch that let every launch's slots fit (0 if none would), given the
+// call's launch count and slot rows per chunk.
+uint64_t chunk_cap(const Call & cx, uint32_t n_launch, uint64_t rows_per_chunk, uint32_t hd) {
+    const uint64_t max_chunks = cx.max_rows(hd) / rows_per_chunk;
+    return n_launch ? max_chunks / n_launch : max_chunks;
 }
 
 // decode calls (<= 8 rows per KV head, q8_0 / q4_0, ggml query rounding, head_dim 128): dec_kernel over (tile group,
-// head pair) items - group c of G takes the call's 32-key tiles c, c + G, ... - about PA_HIP_TARGET_WG workgroups per
-// launch (pages in groups of MAXP), then the merge kernel
-int attn_decode(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+// head pair) items - group c of G takes the launch's 32-key tiles c, c + G, ... - about DEC_TARGET_WG workgroups per
+// launch, then the merge kernel
+int attn_decode(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
                 const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
-    const uint32_t qr = 8, tile = 32;
-    // pages above 2^20 keys are split (the kernel's per-tile buffer ranges are 32-bit byte counts)
-    std::vector<const void *> kpx, vpx;
-    std::vector<uint32_t> nkx;
-    for (int i = 0; i < n_pages; i++) {
-        uint32_t done = 0;
-        do {
-            const uint32_t c = std::min<uint32_t>(nkeys[i] - done, 1u << 20);
-            kpx.push_back((const uint8_t *) k_pages[i] + (size_t) done * s->rs);
-            vpx.push_back((const uint8_t *) v_pages[i] + (size_t) done * s->rs);
-            nkx.push_back(c);
-            done += c;
-        } while (done < nkeys[i]);
+    const uint32_t qr = 8;
+    const uint64_t rows_per_slot = (uint64_t) s->nkv * qr;
+    // tile groups per head pair: at least two tiles per group unless forced (one-tile groups leave each workgroup's
+    // first-load latency and slot write unhidden: 4096 keys 9.7 us at 256 workgroups against 11.8 us at 512)
+    auto groups = [&](uint64_t tiles, uint64_t cap) {
+        const uint64_t want = cx.dec_groups > 0 ? (uint64_t) cx.dec_groups
+                                                : std::min<uint64_t>(std::max<uint64_t>(1, DEC_TARGET_WG / (s->nkv / 2)), (tiles + 1) / 2);
+        return (uint32_t) std::max<uint64_t>(1, std::min({tiles, want, cap}));
+    };
+    uint32_t n_launch = 0;
+    uint64_t n_slots = 0, cap = ~0ull;
+    for_launches(nkeys, n_pages, [&](int, int, uint64_t tiles, uint64_t) { n_launch++; n_slots += groups(tiles, cap); });
+    if (cx.fixed && !(n_launch == 1 && n_slots == 1) && n_slots * rows_per_slot > cx.max_rows(s->hd)) {
+        cap = chunk_cap(cx, n_launch, rows_per_slot, s->hd);
+        if (cap == 0) { set_err("pa_hip_attn_noalloc: " + std::to_string(n_launch) + " launches need more slots than the scratch holds"); return -1; }
+        n_slots = 0;
+        for_launches(nkeys, n_pages, [&](int, int, uint64_t tiles, uint64_t) { n_slots += groups(tiles, cap); });
     }
-    k_pages = kpx.data(); v_pages = vpx.data(); nkeys = nkx.data(); n_pages = (int) nkx.size();
-    // groups of tiles per head pair (group c takes the tiles c, c + G, ...): about PA_HIP_TARGET_WG workgroups in all
-    const int target = std::max(1, env_int("PA_HIP_TARGET_WG", 1024));
-    const int forced_groups = env_int("PA_HIP_GROUPS", 0);
-    struct launch_t { int p0, np; uint32_t n_groups, slot0; };
-    std::vector<launch_t> L;
-    uint32_t n_slots = 0;
-    for (int p0 = 0; p0 < n_pages; p0 += MAXP) {
-        const int np = std::min(MAXP, n_pages - p0);
-        uint64_t tiles = 0;
-        for (int i = 0; i < np; i++) tiles += (nkeys[p0 + i] + tile - 1) / tile;
-        if (tiles == 0) continue;
-        // at least two tiles per group unless forced: one-tile groups leave each workgroup's first-load latency and
-        // slot write unhidden (4096 keys: 9.7 us at 256 workgroups against 11.8 us at 512 one-tile ones)
-        const uint64_t want = forced_groups > 0 ? (uint64_t) forced_groups
-                                                : std::min<uint64_t>(std::max<uint64_t>(1, (uint64_t) target / (s->nkv / 2)), (tiles + 1) / 2);
-        const uint32_t ng = (uint32_t) std::min<uint64_t>(tiles, want);
-        L.push_back({p0, np, ng, n_slots});
-        n_slots += ng;
-    }
-    const bool direct = L.size() == 1 && L[0].n_groups == 1;
-    if (!direct) {
-        const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
-        const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
-        if (!ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") || !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
-            return -1;
-    }
-    const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
-    ws->ev0 = ws->ev1 = nullptr;
-    for (size_t li = 0; li < L.size(); li++) {
-        const launch_t & ln = L[li];
+    const bool direct = n_launch == 1 && n_slots == 1;
+    if (!direct && !cx.slots(n_slots * rows_per_slot, s->hd, st)) return -1;
+    uint32_t li = 0, slot0 = 0;
+    bool ok = true;
+    for_launches(nkeys, n_pages, [&](int p0, int np, uint64_t tiles, uint64_t) {
+        if (!ok) return;
+        const uint32_t ng = groups(tiles, cap);
         AttnArgs a;
         std::memset(&a, 0, sizeof a);
-        uint32_t acc = 0, tacc = 0;
-        for (int i = 0; i < ln.np; i++) {
-            a.kp[i] = (const uint8_t *) k_pages[ln.p0 + i];
-            a.vp[i] = (const uint8_t *) v_pages[ln.p0 + i];
-            a.pstart[i] = acc;
-            a.cstart[i] = tacc;                                      // tile prefix
-            acc += nkeys[ln.p0 + i];
-            tacc += (nkeys[ln.p0 + i] + tile - 1) / tile;
-        }
-        a.pstart[ln.np] = acc;
-        a.cstart[ln.np] = tacc;
-        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_groups; a.chunk = tile;
-        a.n_items = ln.n_groups * (s->nkv / 2);
-        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = 1; a.slot0 = ln.slot0; a.slots = n_slots;
+        page_table(a, k_pages, v_pages, nkeys, p0, np);
+        a.n_chunks = ng; a.chunk = 32;
+        a.n_items = ng * (s->nkv / 2);
+        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = 1; a.slot0 = slot0;
+        a.slots = (uint32_t) n_slots;
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale;
         a.s_mul = s->scale * 1.4426950408889634f;
-        a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
+        a.q = Q; a.po = cx.po; a.pml = cx.pml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
         // the timing events (if any) at the start of the first and the end of the last decode kernel
-        if (!hip_ok(launch_decode((int) s->fmt, a, grid, st, li == 0 ? ev0 : nullptr, li + 1 == L.size() ? ev1 : nullptr),
-                    "decode launch"))
-            return -1;
-    }
-    if (L.empty()) {   // no keys: the events bracket nothing
-        if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
-        if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
-    }
-    if (!direct && !launch_fold(ws, n_slots, s->nkv, qr, s->rows, (int) s->hd, O, m, l, st)) return -1;
-    return 0;
+        ok = hip_ok(launch_decode((int) s->fmt, a, grid, st, li == 0 ? cx.ev0 : nullptr, li + 1 == n_launch ? cx.ev1 : nullptr),
+                    "decode launch");
+        li++;
+        slot0 += ng;
+    });
+    if (!ok) return -1;
+    if (direct) return 0;
+    MergeArgs ma;
+    ma.po = cx.po; ma.pml = cx.pml; ma.O = O; ma.m = m; ma.l = l;
+    ma.n_slots = (uint32_t) n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+    ma.sst = 1; ma.rst = n_slots;                                    // row-major slots: a row's slots contiguous
+    return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
 }
 
 // many rows per KV head (verify, prefill; head dim 128): mma_kernel over row blocks of 32*NW rows x chunks of tiles
-int attn_mma(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+int attn_mma(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
              const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
-    const int nw_env = env_int("PA_HIP_MMA_NW", 0);
-    // 4 waves up to 128 rows: the 2-wave kernel holds four staging units per thread, needs more than 256 registers and
-    // runs one wave per SIMD
-    const uint32_t nw = nw_env == 2 || nw_env == 4 || nw_env == 8 ? (uint32_t) nw_env : s->rows > 128 ? 8u : 4u;
-    const uint32_t tile = 32;
+    // 8 waves above 128 rows (prefill), 4 otherwise (verify, short verify blocks, f16 decode)
+    const uint32_t nw = s->rows > 128 ? 8u : 4u;
     const uint32_t nrb = (s->rows + 32 * nw - 1) / (32 * nw), qr = nrb * 32 * nw;
     // one row block with waves past the last row: those waves only stage (with several row blocks the full ones set
     // the time, and the staging-only branch would slow them)
-    const bool skip = nrb == 1 && s->rows <= 32 * (nw - 1) && nw >= 4;
+    const bool skip = nrb == 1 && s->rows <= 32 * (nw - 1);
     const uint32_t units = s->nkv * nrb;
-    // key chunks: about PA_HIP_MMA_TARGET workgroups in all; by default one round of resident ones (1 of 8 waves, 2 of
-    // 4, 4 of 2 per CU, 256 CUs): a second, partial round costs more than the extra slots save
-    const int target = std::max(1, env_int("PA_HIP_MMA_TARGET", 256 * 8 / (int) nw));
-    struct launch_t { int p0, np; uint32_t tpc, n_chunks, slot0; };
-    std::vector<launch_t> L;
-    uint32_t n_slots = 0;
-    for (int p0 = 0; p0 < n_pages; p0 += MAXP) {
-        const int np = std::min(MAXP, n_pages - p0);
-        uint64_t tiles = 0;
-        for (int i = 0; i < np; i++) tiles += (nkeys[p0 + i] + tile - 1) / tile;
-        if (tiles == 0) continue;
-        const uint64_t want = std::max<uint64_t>(1, (uint64_t) target / units);
-        const uint64_t tpc = (tiles + want - 1) / want;
-        const uint32_t nch = (uint32_t) ((tiles + tpc - 1) / tpc);
-        L.push_back({p0, np, (uint32_t) tpc, nch, n_slots});
-        n_slots += nch;
+    const uint64_t rows_per_slot = (uint64_t) s->nkv * qr;
+    // key chunks: by default one round of resident workgroups (one of 8 waves or two of 4 per CU, 256 CUs); a second,
+    // partial round costs more than the extra slots save
+    const uint64_t target = cx.mma_workgroups > 0 ? (uint64_t) cx.mma_workgroups : 256u * 8 / nw;
+    auto chunking = [&](uint64_t tiles, uint64_t cap, uint32_t & tpc) {
+        const uint64_t want = std::max<uint64_t>(1, std::min(target / units, cap));
+        tpc = (uint32_t) ((tiles + want - 1) / want);
+        return (uint32_t) ((tiles + tpc - 1) / tpc);
+    };
+    uint32_t n_launch = 0, tpc = 0;
+    uint64_t n_slots = 0, cap = ~0ull;
+    for_launches(nkeys, n_pages, [&](int, int, uint64_t tiles, uint64_t) { n_launch++; n_slots += chunking(tiles, cap, tpc); });
+    if (cx.fixed && !(n_launch == 1 && n_slots == 1) && n_slots * rows_per_slot > cx.max_rows(s->hd)) {
+        cap = chunk_cap(cx, n_launch, rows_per_slot, s->hd);
+        if (cap == 0) { set_err("pa_hip_attn_noalloc: " + std::to_string(n_launch) + " launches need more slots than the scratch holds"); return -1; }
+        n_slots = 0;
+        for_launches(nkeys, n_pages, [&](int, int, uint64_t tiles, uint64_t) { n_slots += chunking(tiles, cap, tpc); });
     }
-    const bool direct = L.size() == 1 && L[0].n_chunks == 1;
-    if (!direct) {
-        const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
-        const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
-        if (!ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") || !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
-            return -1;
-    }
-    const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
-    ws->ev0 = ws->ev1 = nullptr;
-    for (size_t li = 0; li < L.size(); li++) {
-        const launch_t & ln = L[li];
+    const bool direct = n_launch == 1 && n_slots == 1;
+    if (!direct && !cx.slots(n_slots * rows_per_slot, s->hd, st)) return -1;
+    uint32_t li = 0, slot0 = 0;
+    bool ok = true;
+    for_launches(nkeys, n_pages, [&](int p0, int np, uint64_t tiles, uint64_t) {
+        if (!ok) return;
+        const uint32_t nch = chunking(tiles, cap, tpc);
         AttnArgs a;
         std::memset(&a, 0, sizeof a);
-        uint32_t acc = 0, tacc = 0;
-        for (int i = 0; i < ln.np; i++) {
-            a.kp[i] = (const uint8_t *) k_pages[ln.p0 + i];
-            a.vp[i] = (const uint8_t *) v_pages[ln.p0 + i];
-            a.pstart[i] = acc;
-            a.cstart[i] = tacc;
-            acc += nkeys[ln.p0 + i];
-            tacc += (nkeys[ln.p0 + i] + tile - 1) / tile;
-        }
-        a.pstart[ln.np] = acc;
-        a.cstart[ln.np] = tacc;
-        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.tpc;
-        a.n_items = ln.n_chunks * units;
-        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
-        a.slots = n_slots;
+        page_table(a, k_pages, v_pages, nkeys, p0, np);
+        a.n_chunks = nch; a.chunk = tpc;
+        a.n_items = nch * units;
+        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = slot0;
+        a.slots = (uint32_t) n_slots;
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale; a.s_mul = 1.4426950408889634f;
-        a.q = Q; a.po = ws->po; a.pml = ws->pml; a.O = O; a.m = m; a.l = l;
+        a.q = Q; a.po = cx.po; a.pml = cx.pml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
-        if (!hip_ok(launch_mma((int) s->fmt, (int) nw, skip, a, grid, st, li == 0 ? ev0 : nullptr, li + 1 == L.size() ? ev1 : nullptr),
-                    "mma launch"))
-            return -1;
+        ok = hip_ok(launch_mma((int) s->fmt, (int) nw, skip, a, grid, st, li == 0 ? cx.ev0 : nullptr,
+                               li + 1 == n_launch ? cx.ev1 : nullptr), "mma launch");
+        li++;
+        slot0 += nch;
+    });
+    if (!ok) return -1;
+    if (direct) return 0;
+    MergeArgs ma;
+    ma.po = cx.po; ma.pml = cx.pml; ma.O = O; ma.m = m; ma.l = l;
+    ma.n_slots = (uint32_t) n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+    ma.sst = 1; ma.rst = n_slots;
+    return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
+}
+
+// head dim 256 (the reference's compile-time shape): attn_kernel over (key chunk, head, row block) items, chunks of
+// keys that may span pages, about GEN_TARGET_WG workgroups per launch, slot-major slots
+int attn_generic(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+                 const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
+    const int cfg = s->rows <= 16 ? CFG_DECODE : CFG_MID;
+    int rows_wg = 16, nb = 64;
+    cfg_geometry(cfg, rows_wg, nb);
+    const uint32_t nrb = (s->rows + rows_wg - 1) / rows_wg, qr = nrb * rows_wg;
+    const uint32_t units = s->nkv * nrb;
+    const uint64_t rows_per_slot = (uint64_t) s->nkv * qr;
+    // one round of resident workgroups (8 rows x 4 KV heads x 65k q8_0 keys: 82 us at 256, against 112 us at 1024)
+    const uint64_t target = cx.mma_workgroups > 0 ? (uint64_t) cx.mma_workgroups : (uint64_t) GEN_TARGET_WG;
+    auto chunking = [&](uint64_t keys, uint64_t cap, uint32_t & chunk) {
+        const uint64_t want = std::max<uint64_t>(1, std::min(target / units, cap));
+        uint64_t c = (keys + want - 1) / want;
+        c = std::max<uint64_t>((uint64_t) nb, (c + nb - 1) / nb * nb);
+        chunk = (uint32_t) c;
+        return (uint32_t) ((keys + c - 1) / c);
+    };
+    uint32_t n_launch = 0, chunk = 0;
+    uint64_t n_slots = 0, cap = ~0ull;
+    for_launches(nkeys, n_pages, [&](int, int, uint64_t, uint64_t keys) { n_launch++; n_slots += chunking(keys, cap, chunk); });
+    if (cx.fixed && !(n_launch == 1 && n_slots == 1) && n_slots * rows_per_slot > cx.max_rows(s->hd)) {
+        cap = chunk_cap(cx, n_launch, rows_per_slot, s->hd);
+        if (cap == 0) { set_err("pa_hip_attn_noalloc: " + std::to_string(n_launch) + " launches need more slots than the scratch holds"); return -1; }
+        n_slots = 0;
+        for_launches(nkeys, n_pages, [&](int, int, uint64_t, uint64_t keys) { n_slots += chunking(keys, cap, chunk); });
     }
-    if (L.empty()) {
-        if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
-        if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;
+    const bool direct = n_launch == 1 && n_slots == 1;
+    if (!direct && !cx.slots(n_slots * rows_per_slot, s->hd, st)) return -1;
+    if (cx.ev0 && !hip_ok(hipEventRecord(cx.ev0, st), "hipEventRecord")) return -1;
+    uint32_t slot0 = 0;
+    bool ok = true;
+    for_launches(nkeys, n_pages, [&](int p0, int np, uint64_t, uint64_t keys) {
+        if (!ok) return;
+        const uint32_t nch = chunking(keys, cap, chunk);
+        AttnArgs a;
+        std::memset(&a, 0, sizeof a);
+        page_table(a, k_pages, v_pages, nkeys, p0, np);
+        a.n_chunks = nch; a.chunk = chunk;
+        a.n_items = nch * units;
+        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = slot0;
+        a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale;
+        a.s_mul = (s->qmode == PA_QMODE_GGML ? s->scale : 1.0f) * 1.4426950408889634f;
+        a.q = Q; a.po = cx.po; a.pml = cx.pml; a.O = O; a.m = m; a.l = l;
+        const uint32_t grid = (a.n_items + 7) / 8 * 8;
+        ok = hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch");
+        slot0 += nch;
+    });
+    if (!ok) return -1;
+    if (cx.ev1 && !hip_ok(hipEventRecord(cx.ev1, st), "hipEventRecord")) return -1;   // the attention kernel alone
+    if (direct) return 0;
+    MergeArgs ma;
+    ma.po = cx.po; ma.pml = cx.pml; ma.O = O; ma.m = m; ma.l = l;
+    ma.n_slots = (uint32_t) n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
+    ma.sst = (uint64_t) s->nkv * qr; ma.rst = 1;                     // slot-major slots
+    return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
+}
+
+// the argument checks every engine-path attention call shares; false (with the message set) on a bad argument
+// (the message strings are built on the error path only: a good call allocates nothing on the host either)
+bool attn_args_ok(const char * fn, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+                  const uint32_t * nkeys, int n_pages, const float * Q, const float * O, const float * m, const float * l) {
+    auto bad = [&](const std::string & why) { set_err(std::string(fn) + ": " + why); return false; };
+    if (!s) return bad("null shape");
+    if (s->hd != 128 && s->hd != 256) return bad("hd must be 128 or 256");
+    if (s->fmt > PA_FMT_Q4_0) return bad("fmt must be 0 (f16), 1 (q8_0) or 2 (q4_0)");
+    if (s->qmode > PA_QMODE_F16) return bad("qmode must be 0 (ggml) or 1 (f16)");
+    if (s->nkv == 0 || s->rows == 0) return bad("nkv and rows must be > 0");
+    const uint32_t hbmin = head_bytes((int) s->fmt, (int) s->hd);
+    if (s->hb < hbmin || (uint64_t) s->rs < (uint64_t) s->nkv * s->hb)
+        return bad("hb " + std::to_string(s->hb) + " / rs " + std::to_string(s->rs) + " too small for nkv " +
+                   std::to_string(s->nkv) + " heads of " + std::to_string(hbmin) + " bytes");
+    // a kernel's per-tile buffer range spans at most 32 rows of rs bytes in 32 bits
+    if (s->rs >= (1u << 26)) return bad("rs must be below 2^26 bytes");
+    if (n_pages < 0 || (n_pages > 0 && (!k_pages || !v_pages || !nkeys))) return bad("bad page table");
+    if (!Q || !O || !m || !l) return bad("null Q/O/m/l");
+    if (((uintptr_t) O & 15) || ((uintptr_t) Q & 3)) return bad("O must be 16-byte and Q 4-byte aligned");
+    uint64_t total = 0;
+    for (int i = 0; i < n_pages; i++) {
+        if (nkeys[i] > 0 && (!k_pages[i] || !v_pages[i])) return bad("null page " + std::to_string(i));
+        total += nkeys[i];
     }
-    if (!direct && !launch_fold(ws, n_slots, s->nkv, qr, s->rows, (int) s->hd, O, m, l, st)) return -1;
-    return 0;
+    if (total > 0xffffffffull) return bad("more than 2^32 - 1 keys");
+    return true;
+}
+
+// the kernel path of a checked call
+int attn_dispatch(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+                  const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
+    // decode: <= 8 rows per KV head, quantized K/V with heads packed back to back, an even head count (the last head's
+    // 16-byte aligned slice then ends with the row), 16-byte rows
+    if (s->qmode == PA_QMODE_GGML && (s->fmt == PA_FMT_Q8_0 || s->fmt == PA_FMT_Q4_0) && s->hd == 128 && s->rows <= 8 &&
+        s->hb == head_bytes((int) s->fmt, 128) && s->nkv % 2 == 0 && s->rs % 16 == 0)
+        return attn_decode(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
+    // every other head-dim-128 call (verify, prefill, f16 K/V, odd head counts, padded heads)
+    if (s->hd == 128) return attn_mma(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
+    return attn_generic(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
+}
+
+// no keys at all: (0, -inf, 0) by the merge kernel over zero slots (nothing else is launched)
+int attn_empty(Call & cx, const pa_hip_shape * s, float * O, float * m, float * l, hipStream_t st) {
+    if (cx.ev0 && !hip_ok(hipEventRecord(cx.ev0, st), "hipEventRecord")) return -1;
+    if (cx.ev1 && !hip_ok(hipEventRecord(cx.ev1, st), "hipEventRecord")) return -1;
+    MergeArgs ma;
+    ma.po = nullptr; ma.pml = nullptr; ma.O = O; ma.m = m; ma.l = l;
+    ma.n_slots = 0; ma.nkv = s->nkv; ma.qr = s->rows; ma.rows = s->rows;
+    ma.sst = 0; ma.rst = 0;
+    return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
+}
+
+int attn_call(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
+              const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
+    uint64_t total = 0;
+    for (int i = 0; i < n_pages; i++) total += nkeys[i];
+    if (total == 0) return attn_empty(cx, s, O, m, l, st);
+    return attn_dispatch(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
 }
 
 }  // namespace
 
+namespace pa_hip {
+
+void set_error(const std::string & e) { set_err(e); }
+
+int attn_fixed_scratch(char * scratch, size_t cap, const pa_hip_shape * s, const void * const * k_pages,
+                       const void * const * v_pages, const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m,
+                       float * l, hipStream_t st) {
+    if (!scratch || cap < 4096) { set_err("pa_hip_attn_noalloc: no scratch"); return -1; }
+    if (!attn_args_ok("pa_hip_attn_noalloc", s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l)) return -1;
+    Call cx;
+    cx.fixed = scratch;
+    cx.cap = cap;
+    return attn_call(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
+}
+
+}  // namespace pa_hip
+
 extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
                            const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, void * stream) {
-    if (!ws || !s) { set_err("pa_hip_attn: null workspace or shape"); return -1; }
-    if (s->hd != 128 && s->hd != 256) { set_err("pa_hip_attn: hd must be 128 or 256"); return -1; }
-    if (s->fmt > PA_FMT_Q4_0) { set_err("pa_hip_attn: fmt must be 0 (f16), 1 (q8_0) or 2 (q4_0)"); return -1; }
-    if (s->qmode > PA_QMODE_F16) { set_err("pa_hip_attn: qmode must be 0 (ggml) or 1 (f16)"); return -1; }
-    if (s->nkv == 0 || s->rows == 0) { set_err("pa_hip_attn: nkv and rows must be > 0"); return -1; }
-    const uint32_t hbmin = head_bytes((int) s->fmt, (int) s->hd);
-    if (s->hb < hbmin || (uint64_t) s->rs < (uint64_t) s->nkv * s->hb) {
-        set_err("pa_hip_attn: hb " + std::to_string(s->hb) + " / rs " + std::to_string(s->rs) + " too small for nkv " +
-                std::to_string(s->nkv) + " heads of " + std::to_string(hbmin) + " bytes");
-        return -1;
-    }
-    if (n_pages < 0 || (n_pages > 0 && (!k_pages || !v_pages || !nkeys))) { set_err("pa_hip_attn: bad page table"); return -1; }
-    if (!Q || !O || !m || !l) { set_err("pa_hip_attn: null Q/O/m/l"); return -1; }
-    if (((uintptr_t) O & 15) || ((uintptr_t) Q & 3)) { set_err("pa_hip_attn: O must be 16-byte and Q 4-byte aligned"); return -1; }
-    uint64_t total = 0;
-    for (int i = 0; i < n_pages; i++) {
-        if (nkeys[i] > 0 && (!k_pages[i] || !v_pages[i])) { set_err("pa_hip_attn: null page " + std::to_string(i)); return -1; }
-        total += nkeys[i];
-    }
-    if (total > 0xffffffffull) { set_err("pa_hip_attn: more than 2^32 keys"); return -1; }
-    hipStream_t st = (hipStream_t) stream;
-    // decode: <= 8 rows per KV head, quantized K/V with heads packed back to back, an even head count (the last head's
-    // 16-byte aligned slice then ends with the row), 16-byte rows
-    if (s->qmode == PA_QMODE_GGML && (s->fmt == PA_FMT_Q8_0 || s->fmt == PA_FMT_Q4_0) && s->hd == 128 && s->rows <= 8 &&
-        s->hb == head_bytes((int) s->fmt, 128) && s->nkv % 2 == 0 && s->rs % 16 == 0 && env_int("PA_HIP_DEC2", 1) != 0)
-        return attn_decode(ws, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
-    // more rows (verify, prefill), head dim 128, heads packed at hb >= the head size, 16-byte aligned Q rows
-    if (s->hd == 128 && env_int("PA_HIP_MMA", 1) != 0)
-        return attn_mma(ws, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
-
-    const int cfg = pick_cfg(s->rows, s->hd);
-    int rows_wg = 16, nb = 64;
-    cfg_geometry(cfg, (int) s->hd, rows_wg, nb);
-    const uint32_t nrb = (s->rows + rows_wg - 1) / rows_wg, qr = nrb * rows_wg;
-    const uint32_t units = s->nkv * nrb;
-
-    // split-K chunking per launch (pages go in groups of MAXP): about one workgroup per CU (PA_HIP_TARGET_WG), a chunk a
-    // multiple of the key tile; a chunk may span pages
-    // At head dim 256 the decode tile's 139 KB of LDS allow one workgroup per CU, so 256 is one round (8 rows x 4 KV
-    // heads x 65k q8_0 keys: 82 us, against 112 us at 1024); the 64-row workgroups measure best at 256 too.
-    const int target = env_int("PA_HIP_TARGET_WG", cfg == CFG_DECODE && s->hd != 256
-                                                       ? (decode_variant() == 2 ? 256 : decode_variant() == 1 ? 1024 : 512) : 256);
-    const int forced_chunk = env_int("PA_HIP_CHUNK", 0);
-    struct launch_t { int p0, np; uint32_t keys, chunk, n_chunks, slot0; };
-    std::vector<launch_t> L;
-    uint32_t n_slots = 0;
-    for (int p0 = 0; p0 < n_pages; p0 += MAXP) {
-        const int np = std::min(MAXP, n_pages - p0);
-        uint32_t keys = 0;
-        for (int i = 0; i < np; i++) keys += nkeys[p0 + i];
-        if (keys == 0) continue;
-        uint32_t chunk;
-        if (forced_chunk > 0) chunk = (uint32_t) forced_chunk;
-        else {
-            const uint32_t want = std::max<uint32_t>(1, (uint32_t) target / units);
-            chunk = (keys + want - 1) / want;
-        }
-        chunk = std::max<uint32_t>((uint32_t) nb, (chunk + nb - 1) / nb * nb);
-        const uint32_t nch = (keys + chunk - 1) / chunk;
-        L.push_back({p0, np, keys, chunk, nch, n_slots});
-        n_slots += nch;
-    }
-    // a separate merge kernel folds the slots (PA_HIP_SEPARATE_FOLD=0: the last workgroups of a single launch do)
-    const bool fused = L.size() <= 1 && env_int("PA_HIP_SEPARATE_FOLD", 1) == 0;
-
-    // buffers: split-K slots and the fold counters
-    const size_t po_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * s->hd * sizeof(float);
-    const size_t pml_b = (size_t) std::max<uint32_t>(n_slots, 1) * s->nkv * qr * sizeof(float2);
-    if (!ensure(ws->po, ws->po_cap, po_b, "hipMalloc partials") || !ensure(ws->pml, ws->pml_cap, pml_b, "hipMalloc partial stats"))
-        return -1;
-    const uint32_t n_groups = L.empty() ? 1 : (L[0].n_chunks + 7) / 8;   // first-level fold groups of 8 chunks
-    const size_t go_b = (size_t) n_groups * s->nkv * qr * s->hd * sizeof(float);
-    const size_t gml_b = (size_t) n_groups * s->nkv * qr * sizeof(float2);
-    if (!ensure(ws->go, ws->go_cap, go_b, "hipMalloc group slots") || !ensure(ws->gml, ws->gml_cap, gml_b, "hipMalloc group stats"))
-        return -1;
-    const size_t ctr_b = (size_t) units * (n_groups + 1) * sizeof(unsigned int);
-    if (ctr_b > ws->ctr_cap) {
-        if (!ensure(ws->ctr, ws->ctr_cap, std::max<size_t>(ctr_b, 4096), "hipMalloc counters") ||
-            !hip_ok(hipMemset(ws->ctr, 0, ws->ctr_cap), "hipMemset counters"))   // once per growth; kernels keep them zero
-            return -1;
-    }
-
-    const hipEvent_t ev0 = ws->ev0, ev1 = ws->ev1;
+    if (!ws) { set_err("pa_hip_attn: null workspace"); return -1; }
+    if (!attn_args_ok("pa_hip_attn", s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l)) return -1;
+    Call cx;
+    cx.ws = ws;
+    cx.dec_groups = ws->dec_groups; cx.mma_workgroups = ws->mma_workgroups;
+    cx.ev0 = ws->ev0; cx.ev1 = ws->ev1;
     ws->ev0 = ws->ev1 = nullptr;
-    if (ev0 && !hip_ok(hipEventRecord(ev0, st), "hipEventRecord")) return -1;
-    if (L.empty()) {   // no keys: the fold of zero slots writes (0, -inf, 0)
-        MergeArgs ma;
-        ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
-        ma.n_slots = 0; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
-        ma.sst = (uint64_t) s->nkv * qr; ma.rst = 1;
-        reply_target(ws, ma);
-        if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
-    }
-    for (const launch_t & ln : L) {
-        AttnArgs a;
-        std::memset(&a, 0, sizeof a);
-        uint32_t acc = 0;
-        for (int i = 0; i < ln.np; i++) {
-            a.kp[i] = (const uint8_t *) k_pages[ln.p0 + i];
-            a.vp[i] = (const uint8_t *) v_pages[ln.p0 + i];
-            a.pstart[i] = acc;
-            acc += nkeys[ln.p0 + i];
-        }
-        a.pstart[ln.np] = acc;
-        a.n_pages = (uint32_t) ln.np; a.n_chunks = ln.n_chunks; a.chunk = ln.chunk;
-        a.n_items = ln.n_chunks * units;
-        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = ln.slot0;
-        a.qmode = s->qmode; a.fused = fused ? 1u : 0u; a.scale = s->scale;
-        a.s_mul = (s->qmode == PA_QMODE_GGML ? s->scale : 1.0f) * 1.4426950408889634f;
-        a.q = Q; a.po = ws->po; a.pml = ws->pml; a.counters = ws->ctr; a.go = ws->go; a.gml = ws->gml; a.O = O; a.m = m; a.l = l;
-        const uint32_t grid = (a.n_items + 7) / 8 * 8;
-        if (!hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch")) return -1;
-    }
-    if (ev1 && !hip_ok(hipEventRecord(ev1, st), "hipEventRecord")) return -1;   // the attention kernel alone
-    if (!fused) {   // attn_kernel slots: slot-major
-        MergeArgs ma;
-        ma.po = ws->po; ma.pml = ws->pml; ma.O = O; ma.m = m; ma.l = l;
-        ma.n_slots = n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
-        ma.sst = (uint64_t) s->nkv * qr; ma.rst = 1;
-        reply_target(ws, ma);
-        if (!hip_ok(launch_merge((int) s->hd, ma, st), "merge launch")) return -1;
-    }
-    return 0;
+    return attn_call(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, (hipStream_t) stream);
 }
 
 extern "C" int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, int64_t vocab, const int32_t * draft, int32_t * out,
@@ -465,10 +525,9 @@ extern "C" int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, i
     if (n_rows < 1 || n_rows > 64) { set_err("pa_hip_accept: n_rows must be 1..64"); return -1; }
     if (vocab < 1 || vocab > 0x7fffffffLL) { set_err("pa_hip_accept: vocab must be 1..2^31-1"); return -1; }
     if ((vocab & 3) == 0 && ((uintptr_t) logits & 15)) { set_err("pa_hip_accept: logits must be 16-byte aligned"); return -1; }
-    // about 256 workgroups in total, each slice at least 4096 values
     const int splits = (int) ((vocab + ACCEPT_SEG - 1) / ACCEPT_SEG);   // ACCEPT_SEG values per workgroup (the kernel's slice)
     const size_t need = (size_t) n_rows * splits * sizeof(unsigned long long);
-    if (!ensure(ws->apart, ws->apart_cap, need, "hipMalloc accept partials")) return -1;
+    if (!ensure(ws, ws->apart, ws->apart_cap, need, (hipStream_t) stream, true, "hipMalloc accept partials")) return -1;
     AcceptArgs a;
     a.logits = logits; a.draft = draft; a.out = out; a.part = ws->apart; a.counter = ws->acount;
     a.vocab = vocab; a.n_rows = n_rows; a.splits = splits;
@@ -479,23 +538,28 @@ extern "C" int pa_hip_accept(pa_hip_ws * ws, const float * logits, int n_rows, i
 extern "C" int pa_hip_attn_reply(pa_hip_ws * ws, const pa_hip_shape * s, const void * const * k_pages,
                                  const void * const * v_pages, const uint32_t * nkeys, int n_pages, const float * Q,
                                  uint16_t * Oh, float * lse, void * stream) {
-    if (!ws || !s) { set_err("pa_hip_attn_reply: null workspace or shape"); return -1; }
+    if (!ws) { set_err("pa_hip_attn_reply: null workspace"); return -1; }
     if (!Oh || !lse) { set_err("pa_hip_attn_reply: null Oh/lse"); return -1; }
     if ((uintptr_t) Oh & 7) { set_err("pa_hip_attn_reply: Oh must be 8-byte aligned"); return -1; }
-    if (s->hd != 128 && s->hd != 256) { set_err("pa_hip_attn_reply: hd must be 128 or 256"); return -1; }
+    if (!s || (s->hd != 128 && s->hd != 256)) { set_err("pa_hip_attn_reply: hd must be 128 or 256"); return -1; }
+    hipStream_t st = (hipStream_t) stream;
     const size_t rows = (size_t) s->nkv * s->rows;
-    if (!ensure(ws->ro, ws->ro_cap, std::max<size_t>(rows, 1) * s->hd * sizeof(float), "hipMalloc reply O") ||
-        !ensure(ws->rml, ws->rml_cap, std::max<size_t>(rows, 1) * 2 * sizeof(float), "hipMalloc reply m, l"))
+    if (!ensure(ws, ws->ro, ws->ro_cap, std::max<size_t>(rows, 1) * s->hd * sizeof(float), st, true, "hipMalloc reply O") ||
+        !ensure(ws, ws->rml, ws->rml_cap, std::max<size_t>(rows, 1) * 2 * sizeof(float), st, true, "hipMalloc reply m, l"))
         return -1;
-    ws->reply_oh = Oh; ws->reply_lse = lse; ws->reply_done = false;
-    const int rc = pa_hip_attn(ws, s, k_pages, v_pages, nkeys, n_pages, Q, ws->ro, ws->rml, ws->rml + rows, stream);
-    const bool done = ws->reply_done;
-    ws->reply_oh = nullptr; ws->reply_lse = nullptr; ws->reply_done = false;
+    float * O = ws->ro, * m = ws->rml, * l = ws->rml + rows;
+    if (!attn_args_ok("pa_hip_attn_reply", s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l)) return -1;
+    Call cx;
+    cx.ws = ws;
+    cx.dec_groups = ws->dec_groups; cx.mma_workgroups = ws->mma_workgroups;
+    cx.ev0 = ws->ev0; cx.ev1 = ws->ev1;
+    ws->ev0 = ws->ev1 = nullptr;
+    cx.reply_oh = Oh; cx.reply_lse = lse;
+    const int rc = attn_call(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
     if (rc != 0) return rc;
-    if (done) return 0;                                               // the split-K merge wrote the reply
+    if (cx.reply_done) return 0;                                      // the split-K merge wrote the reply
     // a single-chunk call wrote (O, m, l) directly: normalise them
-    return hip_ok(launch_normalise((int) s->hd, ws->ro, ws->rml, ws->rml + rows, rows, Oh, lse, (hipStream_t) stream),
-                  "normalise launch") ? 0 : -1;
+    return hip_ok(launch_normalise((int) s->hd, O, m, l, rows, Oh, lse, st), "normalise launch") ? 0 : -1;
 }
 
 namespace {
@@ -636,6 +700,8 @@ extern "C" int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, vo
 namespace {
 
 std::atomic<int> g_nr{0}, g_hd{0};
+int env_int(const char * name, int def) { const char * e = getenv(name); return e ? atoi(e) : def; }
+// read once per process: the environment (PA_NR, PA_HD) or the reference's compile-time NR = 48, HD = 256
 void compat_shape(int & nr, int & hd) {
     if (g_nr.load() == 0) {
         const int a = env_int("PA_NR", 48), b = env_int("PA_HD", 256);
@@ -679,19 +745,21 @@ bool compat_call(pa_hip_ws * w, const float * Q, int qrs, int qhs, const uint8_t
     const size_t span = (size_t) (nk - 1) * rs + (size_t) (nkv - 1) * hb + hbmin;
     const uint8_t * dK = K, * dV = V;
     if (!is_device_ptr(K)) {
-        if (!ensure(w->dk, w->dk_cap, span, "hipMalloc K staging") ||
+        if (!ensure(w, w->dk, w->dk_cap, span, st, false, "hipMalloc K staging") ||
             !hip_ok(hipMemcpyAsync(w->dk, K, span, hipMemcpyHostToDevice, st), "K upload"))
             return false;
         dK = w->dk;
     }
     if (!is_device_ptr(V)) {
-        if (!ensure(w->dv, w->dv_cap, span, "hipMalloc V staging") ||
+        if (!ensure(w, w->dv, w->dv_cap, span, st, false, "hipMalloc V staging") ||
             !hip_ok(hipMemcpyAsync(w->dv, V, span, hipMemcpyHostToDevice, st), "V upload"))
             return false;
         dV = w->dv;
     }
     const size_t q_b = rows * HD * sizeof(float), o_b = rows * (HD + 2) * sizeof(float);
-    if (!ensure(w->dq, w->dq_cap, q_b, "hipMalloc Q staging") || !ensure(w->dout, w->dout_cap, o_b, "hipMalloc O staging")) return false;
+    if (!ensure(w, w->dq, w->dq_cap, q_b, st, false, "hipMalloc Q staging") ||
+        !ensure(w, w->dout, w->dout_cap, o_b, st, false, "hipMalloc O staging"))
+        return false;
     for (int h = 0; h < nkv; h++)
         if (!hip_ok(hipMemcpy2DAsync(w->dq + (size_t) h * NR * HD, HD * sizeof(float), Q + (size_t) h * qhs, (size_t) qrs * sizeof(float),
                                      HD * sizeof(float), NR, hipMemcpyHostToDevice, st), "Q upload"))

@@ -3,11 +3,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
+#include "../../include/phone_attn_hip.h"
+
 namespace pa_hip {
 
 constexpr int MAXP = 64;   // pages per attention launch (more are split over several launches into one slot array)
 
-enum { CFG_DECODE = 0, CFG_MID = 1, CFG_VERIFY = 2, CFG_PREFILL = 3 };   // 16 / 64 / 128 / 128 rows per workgroup
+enum { CFG_DECODE = 0, CFG_MID = 1 };   // head dim 256 (attn_kernel): 16 / 64 rows per workgroup
 
 struct AttnArgs {
     const uint8_t * kp[MAXP];       // page base (key 0, head 0) of K / V
@@ -23,15 +27,12 @@ struct AttnArgs {
     uint32_t slot0;                 // slot of chunk 0 of this launch
     uint32_t slots;                 // decode / MMA kernels: the call's slot count (slots are row-major: [head, row][slot])
     uint32_t qmode;                 // PA_QMODE_GGML / PA_QMODE_F16
-    uint32_t fused;                 // 1: this launch holds every chunk; the last workgroup per (head, row block) folds
+    uint32_t fused;                 // 1: this launch holds every chunk of the call (a single chunk writes the result)
     float scale;                    // softmax scale (PA_QMODE_F16 folds it into Q)
     float s_mul;                    // factor from the dot to base-2 logits (scale * log2 e, or log2 e)
     const float * q;                // [nkv][rows][hd] fp32
     float * po;                     // slots [nkv][qr][slots][hd] (decode, MMA) or [slot][nkv][qr][hd] (attn_kernel)
     float2 * pml;                   // the same without hd: (max in base-2 units, sum)
-    unsigned int * counters;        // [nkv][nrb][n_groups + 1] fold counters, zero between calls
-    float * go;                     // first-level fold (group) slots [group][nkv][qr][hd]
-    float2 * gml;                   // [group][nkv][qr]
     float * O, * m, * l;            // final [nkv][rows][hd], [nkv][rows]
 };
 
@@ -68,8 +69,7 @@ hipError_t launch_normalise(int hd, const float * O, const float * m, const floa
                             float * lse, hipStream_t st);
 hipError_t launch_coattn(int hd, const uint16_t * Oh, const float * lse, const float * Oloc, const float * mloc,
                          const float * lloc, uint64_t rows, float * out, float * lse_out, hipStream_t st);
-void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb);
-int decode_variant();
+void cfg_geometry(int cfg, int & rows_per_wg, int & nb);
 
 #ifndef PA_ACCEPT_SEG
 #define PA_ACCEPT_SEG 16384
@@ -88,5 +88,13 @@ struct AcceptArgs {
     int n_rows, splits;
 };
 hipError_t launch_accept(const AcceptArgs & a, hipStream_t st);
+
+// host side (pa_abi.cpp): the calling thread's last error, and the engine-path call with its split-K slots in a fixed
+// device array of `cap` bytes instead of a workspace (nothing allocated; the split adapts so the slots fit, and a call
+// whose launches cannot fit one slot set each is refused)
+void set_error(const std::string & e);
+int attn_fixed_scratch(char * scratch, size_t cap, const pa_hip_shape * s, const void * const * k_pages,
+                       const void * const * v_pages, const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m,
+                       float * l, hipStream_t st);
 
 }  // namespace pa_hip

@@ -11,17 +11,15 @@
 //   O^T (dims x rows) += V^T . P^T,
 // so lane (g, n) holds row n's scores of keys 4g..4g+3 (+16) - exactly the B operand of the PV MFMA - and the running
 // max / sum of row n live in the lanes that own row n. Online softmax is in base 2. WK waves may split the keys of a
-// tile; their states merge through LDS. Each workgroup then writes one split-K slot (O^T unnormalised, base-2 max, sum);
-// the last workgroup of a (head, row block) to finish - a device-scope counter, no waiting - folds the slots into the
-// final (O, m, l). With one chunk the workgroup writes the final result directly.
+// tile; their states merge through LDS. Each workgroup then writes one split-K slot (O^T unnormalised, base-2 max, sum),
+// which a merge kernel folds into the final (O, m, l); with one chunk the workgroup writes the final result directly.
+// This kernel serves head dim 256 (the reference's compile-time shape); head dim 128 runs on dec_kernel / mma_kernel.
 //
 // Reference roles: pa_attn_big + pa_big_load (pa-metal.mm:379-487: per (row tile, KV head, key chunk), dequant a K/V
 // block, S = QK^T, online softmax with key masking, O = alpha O + PV, write a slot) and pa_merge / pa_merge_big
 // (pa-metal.mm:137-159, 490-524: M = max, skip -inf slots, w = exp(m_c - M), O = sum w O_c, L = sum w l_c).
 #include "pa_attn.h"
 #include "pa_common.h"
-
-#include <cstdlib>
 
 namespace pa_hip {
 
@@ -177,71 +175,6 @@ struct TileIt {
     __device__ __forceinline__ bool valid(const AttnArgs & a, uint32_t key_hi) const { return p < a.n_pages && a.pstart[p] + jt < key_hi; }
 };
 
-// ---------------------------------------------------------------- split-K fold helpers
-constexpr uint32_t FOLD_G = 8;   // chunks per first-level fold group
-
-// count this workgroup's arrival at `ctr`; true for the workgroup that completes `expected` arrivals (it resets the
-// counter). Ordering: the barrier completes every wave's stores into the XCD's L2 (workgroup scope); thread 0's
-// increment is a release at device scope (one L2 write-back per workgroup, no invalidate); only the completing
-// workgroup acquires (invalidates), so the streaming workgroups keep their caches.
-template <int NT>
-__device__ __forceinline__ bool fold_arrive(unsigned int * ctr, uint32_t expected, int tid, bool & s_last) {
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned int done = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = done == expected - 1;
-        if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next call
-    }
-    __syncthreads();
-    if (!s_last) return false;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return true;
-}
-
-// fold n slots (slot i of head h, row r at ml[i*sstride + h*qr + r], o[(i*sstride + h*qr + r)*HD]) for rows [r0, r1):
-// online over batches of 8 slots (one round trip each). Writes the final (O, m in natural units, l) or group slot `gs`.
-template <int HD, int NT>
-__device__ __forceinline__ void fold_rows(const AttnArgs & a, uint32_t h, uint32_t r0, uint32_t r1, const float2 * ml, const float * o,
-                                          uint32_t n, size_t sstride, bool final, uint32_t gs, int tid) {
-    for (uint32_t e = tid; e < (r1 - r0) * (HD / 4); e += NT) {
-        const uint32_t row = r0 + e / (HD / 4), d4 = e % (HD / 4);
-        const size_t pr = (size_t) h * a.qr + row;
-        float M = -INFINITY, L = 0.0f;
-        pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (uint32_t s0 = 0; s0 < n; s0 += 8) {
-            float2 mq[8];
-            pa_f4 oq[8];
-            #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const bool in = s0 + q < n;
-                mq[q] = in ? ml[(s0 + q) * sstride + pr] : make_float2(-INFINITY, 0.0f);
-                oq[q] = in ? *(const pa_f4 *) (o + ((s0 + q) * sstride + pr) * HD + 4 * d4) : (pa_f4){0.f, 0.f, 0.f, 0.f};
-            }
-            float Mb = M;
-            #pragma unroll
-            for (int q = 0; q < 8; q++) Mb = fmaxf(Mb, mq[q].x);
-            const float Ms = Mb == -INFINITY ? 0.0f : Mb;
-            const float sc = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Ms);
-            acc *= sc;
-            L *= sc;
-            #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const float wt = __builtin_amdgcn_exp2f(mq[q].x - Ms);   // an empty slot (-inf) weighs 0
-                L += wt * mq[q].y;
-                acc += wt * oq[q];
-            }
-            M = Mb;
-        }
-        if (final) {
-            *(pa_f4 *) (a.O + ((size_t) h * a.rows + row) * HD + 4 * d4) = acc;
-            if (d4 == 0) { a.m[(size_t) h * a.rows + row] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[(size_t) h * a.rows + row] = L; }
-        } else {
-            *(pa_f4 *) (a.go + (gs * sstride + pr) * HD + 4 * d4) = acc;
-            if (d4 == 0) a.gml[gs * sstride + pr] = make_float2(M, L);
-        }
-    }
-}
-
 // ---------------------------------------------------------------- the attention kernel
 template <int HD, int FMT, int RT, int WR, int WK, int NB>
 __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
@@ -256,7 +189,6 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
     constexpr int COMB_LDS = WK > 1 ? WK * ROWS_WG * (HD + 2) * 4 : 0;
     constexpr int LDS = TILE_LDS > COMB_LDS ? TILE_LDS : COMB_LDS;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
-    __shared__ bool s_last;
     _Float16 * Ks = (_Float16 *) smem;
     _Float16 * Vt = Ks + NB * KS;
     float * Ksc = (float *) (Vt + HD * VS);   // [NKD][NB]: K block scale * s_mul
@@ -492,23 +424,6 @@ __global__ __launch_bounds__(64 * WR * WK) void attn_kernel(const AttnArgs a) {
             emit(row, d4, acc, M, L);
         }
     }
-    if (direct || !a.fused) return;
-
-    // ---- fused split-K fold, two levels: the last workgroup to finish in a group of FOLD_G consecutive chunks folds the
-    // group's slots into a group slot; the last group folder folds the group slots into the final (O, m, l). Counters
-    // are device-scope atomics (no waiting); each folder resets the counter it completed.
-    const uint32_t unit = h * a.nrb + rb;
-    const uint32_t n_groups = (a.n_chunks + FOLD_G - 1) / FOLD_G, grp = c / FOLD_G;
-    const uint32_t g0 = grp * FOLD_G, gn = min(a.n_chunks, g0 + FOLD_G) - g0;
-    const size_t sstride = (size_t) a.nkv * a.qr;                    // rows between slots
-    if (!fold_arrive<NT>(a.counters + (size_t) unit * (n_groups + 1) + grp, gn, tid, s_last)) return;
-    // this workgroup folds group `grp` (its slots g0 .. g0+gn-1): into the final result if it is the only group
-    const bool final1 = n_groups == 1;
-    fold_rows<HD, NT>(a, h, rb * ROWS_WG, min(a.rows, (rb + 1) * ROWS_WG), a.pml + g0 * sstride, a.po + g0 * sstride * HD, gn, sstride,
-                      final1, grp, tid);
-    if (final1) return;
-    if (!fold_arrive<NT>(a.counters + (size_t) unit * (n_groups + 1) + n_groups, n_groups, tid, s_last)) return;
-    fold_rows<HD, NT>(a, h, rb * ROWS_WG, min(a.rows, (rb + 1) * ROWS_WG), a.gml, a.go, n_groups, sstride, true, 0, tid);
 }
 
 // ---------------------------------------------------------------- split-K fold as its own kernel
@@ -694,53 +609,25 @@ static hipError_t launch_attn(const AttnArgs & a, uint32_t grid, hipStream_t st)
     return hipGetLastError();
 }
 
-// configurations (RT, WR, WK, NB). Decode: 8 waves split a 256-key tile (16 rows, 8 real). Mid: 64 rows. Verify /
-// prefill: 128 rows. Head dim 256 (the reference shape) keeps to at most 64 rows per workgroup (registers).
-template <int HD, int FMT>
+// configurations (RT, WR, WK, NB) at head dim 256: decode-shaped calls (<= 16 rows per KV head) split each 128-key
+// tile over 4 waves (16 rows, one workgroup per CU by LDS); more rows take 64 rows per workgroup (registers).
+template <int FMT>
 static hipError_t launch_attn_cfg(int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st) {
-    if constexpr (HD == 256) {
-        if (cfg == CFG_DECODE) return launch_attn<HD, FMT, 1, 1, 4, 128>(a, grid, st);
-        return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
-    } else {
-        switch (cfg) {
-            case CFG_DECODE:
-                switch (decode_variant()) {
-                    case 1: return launch_attn<HD, FMT, 1, 1, 2, 64>(a, grid, st);
-                    case 2: return launch_attn<HD, FMT, 1, 1, 8, 256>(a, grid, st);
-                    default: return launch_attn<HD, FMT, 1, 1, 4, 128>(a, grid, st);
-                }
-            case CFG_MID:    return launch_attn<HD, FMT, 1, 4, 1, 64>(a, grid, st);
-            default:         return launch_attn<HD, FMT, 2, 4, 1, 64>(a, grid, st);   // verify / prefill
-        }
-    }
+    if (cfg == CFG_DECODE) return launch_attn<256, FMT, 1, 1, 4, 128>(a, grid, st);
+    return launch_attn<256, FMT, 1, 4, 1, 64>(a, grid, st);
 }
 
 hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st) {
-    if (hd == 128) {
-        if (fmt == 0) return launch_attn_cfg<128, 0>(cfg, a, grid, st);
-        if (fmt == 1) return launch_attn_cfg<128, 1>(cfg, a, grid, st);
-        if (fmt == 2) return launch_attn_cfg<128, 2>(cfg, a, grid, st);
-    } else if (hd == 256) {
-        if (fmt == 0) return launch_attn_cfg<256, 0>(cfg, a, grid, st);
-        if (fmt == 1) return launch_attn_cfg<256, 1>(cfg, a, grid, st);
-        if (fmt == 2) return launch_attn_cfg<256, 2>(cfg, a, grid, st);
-    }
+    if (hd != 256) return hipErrorInvalidValue;
+    if (fmt == 0) return launch_attn_cfg<0>(cfg, a, grid, st);
+    if (fmt == 1) return launch_attn_cfg<1>(cfg, a, grid, st);
+    if (fmt == 2) return launch_attn_cfg<2>(cfg, a, grid, st);
     return hipErrorInvalidValue;
 }
 
-int decode_variant() {
-    static const int v = getenv("PA_HIP_DECODE") ? atoi(getenv("PA_HIP_DECODE")) : 1;
-    return v;
-}
-
-void cfg_geometry(int cfg, int hd, int & rows_per_wg, int & nb) {
-    if (cfg == CFG_DECODE) {
-        rows_per_wg = 16;
-        const int v = decode_variant();
-        nb = hd == 256 ? 128 : v == 1 ? 64 : v == 2 ? 256 : 128;
-    }
-    else if (cfg == CFG_MID || hd == 256) { rows_per_wg = 64; nb = 64; }
-    else { rows_per_wg = 128; nb = 64; }
+void cfg_geometry(int cfg, int & rows_per_wg, int & nb) {
+    if (cfg == CFG_DECODE) { rows_per_wg = 16; nb = 128; }
+    else { rows_per_wg = 64; nb = 64; }
 }
 
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {

@@ -241,7 +241,9 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
         if (tau < T) {
             page_of(tau, pl);
             const uint32_t j0 = 32 * (tau - a.cstart[pl]);
-            tile_load(X, pl, j0, (a.pstart[pl + 1] - a.pstart[pl] - j0) * rs - pr * G::SL);
+            // the range covers the tile's rows only (at most 32 of rs bytes, rs < 2^26 by the host's check), so a page
+            // of any size keeps the 32-bit byte count exact; the pair's slice ends inside each row (nkv * hb <= rs)
+            tile_load(X, pl, j0, min(a.pstart[pl + 1] - a.pstart[pl] - j0, 32u) * rs - pr * G::SL);
         } else {
             tile_load(X, pl, 0, 0u);
         }

@@ -244,7 +244,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     constexpr int PF = 2;                                            // tiles whose raw bytes are in flight
     constexpr int NT = 64 * NW;
     constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
-    static_assert(UPT * NT == 512, "NW must be 2, 4 or 8");
+    static_assert(UPT * NT == 512, "NW must be 4 or 8");
     __shared__ __attribute__((aligned(16))) char smem[2 * MM_STAGE];
 
     // ---- which (chunk, KV head, row block): row blocks fastest, so the workgroups that share a chunk's K/V run side
@@ -278,7 +278,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         if (live) cl.seek(a, tau);
         const uint32_t j0 = live ? 32 * (tau - cl.tb) : 0u;
         const uint32_t last = live ? cl.nk - 1 - j0 : 0u;
-        const uint32_t nrec = live ? (last + 1) * a.rs : 0u;
+        // the range covers the tile's rows only (at most 32 of rs bytes, rs < 2^26 by the host's check), so a page of
+        // any size keeps the 32-bit byte count exact
+        const uint32_t nrec = live ? min(last + 1, 32u) * a.rs : 0u;
         #pragma unroll
         for (int i = 0; i < UPT; i++) {
             const int u = tid + NT * i;
@@ -425,7 +427,6 @@ template <int FMT, bool PRE>
 static hipError_t launch_mma_fmt(int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0,
                                  hipEvent_t ev1) {
     switch (nw) {
-        case 2: hipExtLaunchKernelGGL((mma_kernel<FMT, 2, PRE, false>), dim3(grid), dim3(128), 0, st, ev0, ev1, 0, a); break;
         case 4:
             if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
             else hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);

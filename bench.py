@@ -2,19 +2,30 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--secondary] [--no-cpu]
 
-Headline workload: decode at long context, 64 layers in sequence, each layer = 1 query token x 64
-query heads over 8 KV heads (GQA 8), head dim 128, 131,072 old q8_0 positions in 32 pages of 4,096 keys, K with 4 x8
-outlier channels per head, 64 distinct seeded caches (18.25 GB in HBM, made on the device by libpa_synth). A step is
-one pass over the 64 layers: per layer one pa_hip_attn call (split-K attention kernel + merge kernel) on one stream.
+Headline workload: decode at long context, 64 layers in sequence, each layer = 1 query token x 64 query heads over 8 KV
+heads (GQA 8), head dim 128, 131,072 old q8_0 positions in 32 pages of 4,096 keys, K with 4 x8 outlier channels per
+head, 64 distinct seeded caches (18.25 GB in HBM, made on the device by libpa_synth). A step is one pass over the 64
+layers: per layer one pa_hip_attn call (split-K attention kernel + merge kernel) on one stream.
 
-Printed: ONE JSON line. value = microseconds per layer of the whole call sequence (lower is better), the 64 layers
-captured once as a HIP graph and replayed per step (the eager per-call figure is reported beside it); roofline = the
-decode kernel's algorithmic bytes per launch / its mean duration (start/end events recorded by the kernel launch itself,
-on its stream), traffic = HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
-cpu_baseline = the oracle's ggml-faithful restatement (oracle/pa_oracle.c, OpenMP over rows) timed on this host's cores
-over the first --cpu-layers layers at full size, with the GPU's layer-0 output checked against it (parity_vs_cpu).
---secondary adds the other workloads (4k decode, 16-token verify, 512-token prefill, q4_0 decode/verify, fused
-acceptance) as "secondary" entries.
+Printed: ONE JSON line.
+  value       microseconds per layer of the headline call sequence (lower is better): the 64 layers captured once as a
+              HIP graph and replayed per step (the eager per-call figure is reported beside it);
+  roofline    the decode kernel's algorithmic bytes per launch / its mean duration (start/end events recorded by the
+              kernel launch itself, on its stream); traffic = HBM bytes per launch from the committed rocprofv3
+              FETCH_SIZE / WRITE_SIZE summary (profiles/decode128k_pmc.json);
+  cpu_baseline  the CPU path (oracle/pa_cpu_simd.c: ggml's CPU flash-attention arithmetic for q8_0 / q4_0, vectorized
+              with AVX-512 VNNI or AVX2, equal to the oracle bit for bit) timed on this host's cores over a bounded sample
+              of the workload, with the GPU's layer-0 output checked against it (parity_vs_cpu);
+  prefill     the 512-token prefill chunk (4,096 rows per KV head, 65,536 q8_0 keys, 64 distinct caches): us/layer,
+              TFLOP/s and the fraction of fp16 MFMA nameplate, counters from profiles/prefill_pmc.json, CPU leg over one
+              layer at full size;
+  verify      the 16-token verify block (1,024 rows over 98,304 q8_0 keys, 64 layers): GB/s and the fraction of HBM
+              nameplate, traffic from profiles/verify_pmc.json, CPU leg;
+  decode_q4_0, verify_q4_0, decode_4096, accept   the 4-bit cache (143,360 positions), the 4,096-key decode layer of
+              the ggml-parity workload, and the fused greedy acceptance over fp32 logits [17][151,936] (bit-exact);
+  measured_bw_gbs  plain copy / read of 2 GiB, and read_layer: one launch reading exactly one headline layer's bytes,
+              timed per launch (the practical floor of one decode launch).
+--secondary adds the reply side, KV ingest and the reference's own shape (head dim 256).
 """
 from __future__ import annotations
 
@@ -161,8 +172,10 @@ def time_layers_graph(bb, ws, lay: Layers, steps: int, reps: int = 1):
     return total_ms
 
 
-def measured_copy_bw(bb, nbytes=2 << 30):
-    """Plain device-to-device copy and read-only stream of nbytes: the achievable-bandwidth reference."""
+def measured_bw(bb, layer_bytes: int, nbytes=2 << 30):
+    """The achievable-bandwidth references: a plain device-to-device copy and a read-only stream of nbytes (10 launches
+    back to back), and read_layer: one launch reading exactly layer_bytes (one headline layer's K and V), timed per
+    launch by its own events, mean of 20 - the practical floor of one decode launch, ramp-up and tail included."""
     syn = bb.synth()
     a, b = bb.DeviceBuffer(nbytes), bb.DeviceBuffer(nbytes)
     sink = bb.DeviceBuffer(1 << 16)
@@ -179,61 +192,105 @@ def measured_copy_bw(bb, nbytes=2 << 30):
         syn.pa_synth_event_record(e1, None)
         ms = syn.pa_synth_event_ms(e0, e1) / 10
         res[name] = traffic / (ms * 1e-3) / 1e9
+    # one layer per launch: 7 layer-sized windows of the 2 GiB buffer in turn, so no launch finds its bytes in the
+    # 256 MB last-level cache from the launch before
+    windows = [i * layer_bytes for i in range(nbytes // layer_bytes)]
+    per = []
+    for i in range(22):
+        off = windows[i % len(windows)]
+        syn.pa_synth_event_record(e0, None)
+        syn.pa_synth_read(a.ptr + off, layer_bytes, 4096, sink.ptr, None)
+        syn.pa_synth_event_record(e1, None)
+        ms = syn.pa_synth_event_ms(e0, e1)
+        if i >= 2:
+            per.append(ms)
+    us = float(np.mean(per)) * 1e3
+    res["read_layer"] = layer_bytes / (us * 1e-6) / 1e9
+    res["read_layer_us"] = us
+    syn.pa_synth_event_free(e0); syn.pa_synth_event_free(e1)
     for x in (a, b, sink):
         x.close()
     return res
 
 
-def cpu_baseline(bb, lay: Layers, n_layers: int):
-    """Time the oracle's ggml-faithful CPU restatement over the first n_layers layers of the workload at full size (all
-    keys, all rows, every host core), and check the GPU's layer-0 output against the CPU's on the same bytes."""
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "threads": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline(bb, lay: Layers, n_layers: int, row_step: int = 1):
+    """Time the CPU path (orc_attn_ggml_simd: ggml's CPU flash-attention arithmetic, vectorized, equal to the oracle bit
+    for bit) over the first n_layers layers of the workload at full size (every row_step-th row of each KV head),
+    on every host core, and check the GPU's layer-0 output against the CPU's on the same bytes."""
     import oracle as orc
-    s = orc.make_shape(lay.nkv, lay.rows, lay.hd, lay.fmt)
-    threads = len(os.sched_getaffinity(0))
+    info = cpu_info()
+    threads = info["threads"]
+    sel = np.arange(0, lay.rows, row_step)
+    s = orc.make_shape(lay.nkv, len(sel), lay.hd, lay.fmt)
     r = lay.nkv * lay.rows
     nbytes = lay.n_keys * lay.rs
     total = 0.0
     parity = None
+    path = "?"
     ws = bb.Workspace()
     for L in range(n_layers):
         kb = lay.kv[L][0].download(np.uint8, nbytes)
         vb = lay.kv[L][1].download(np.uint8, nbytes)
-        q = lay.q[L].download(np.float32).reshape(-1, lay.hd)
+        q = lay.q[L].download(np.float32).reshape(lay.nkv, lay.rows, lay.hd)[:, sel, :].reshape(-1, lay.hd)
         t0 = time.perf_counter()
-        O, m, l = orc.attn_ggml(s, q, kb, vb, lay.n_keys, threads)
+        O, m, l, path = orc.attn_ggml_simd(s, q, kb, vb, lay.n_keys, threads)
         total += time.perf_counter() - t0
         if L == 0:
             ws.attn(lay.shape, lay.pages[0], lay.q[0].ptr, lay.O, lay.m, lay.l)
             bb.device_sync()
             ml = lay.out.download(np.float32, 2 * r, offset=r * lay.hd * 4)
             Og = lay.out.download(np.float32, r * lay.hd).reshape(r, lay.hd)
-            eo, em, el = orc.rel_err(Og, ml[:r], ml[r:], O, m, l)
-            parity = {"max_rel_O": eo, "max_rel_m": em, "max_rel_l": el, "layer": 0, "keys": lay.n_keys, "tol": 2e-3}
+            idx = (np.arange(lay.nkv)[:, None] * lay.rows + sel[None, :]).reshape(-1)
+            eo, em, el = orc.rel_err(Og[idx], ml[:r][idx], ml[r:][idx], O, m, l)
+            parity = {"max_rel_O": eo, "max_rel_m": em, "max_rel_l": el, "layer": 0, "keys": lay.n_keys,
+                      "rows_checked": int(len(idx)), "tol": 2e-3}
         del kb, vb
     ws.close()
-    per_layer_us = total * 1e6 / n_layers
-    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"layers 0..{n_layers - 1} of {lay.n_layers} at full size ({lay.n_keys} keys, all {r} rows), "
-                      f"oracle/pa_oracle.c orc_attn_ggml (ggml-faithful: q8_0 int block dots, online softmax, fp32 V "
-                      f"accumulation; OpenMP over rows, {threads} threads), {total:.2f} s of CPU time in all",
+    frac = len(sel) / lay.rows
+    per_layer_us = total * 1e6 / n_layers / frac          # a row sample is scaled to the whole layer
+    sample = f"layers 0..{n_layers - 1} of {lay.n_layers} at full size ({lay.n_keys} keys"
+    sample += f", all {r} rows)" if row_step == 1 else f", every {row_step}th row: {len(sel) * lay.nkv} of {r} rows, time scaled x{row_step})"
+    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": threads, "kind": "port", "simd": path,
+            "cpu_model": info["cpu_model"], "nproc": info["nproc"],
+            "sample": sample + f", oracle/pa_cpu_simd.c orc_attn_ggml_simd (ggml CPU flash-attention arithmetic: q8_0 "
+                               f"query, integer block dots, expf online softmax, fp32 V accumulation; {path}, OpenMP over "
+                               f"rows, {threads} threads), {total:.2f} s of CPU time",
             }, parity
 
 
-def read_traffic(name: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
+def read_pmc(name: str):
+    """The committed rocprofv3 counter summary of a kernel (profiles/<name>_pmc.json), or None."""
     p = ROOT / "profiles" / f"{name}_pmc.json"
     if not p.exists():
         return None
     try:
-        return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+        return json.loads(p.read_text())
     except Exception:
         return None
 
 
-def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label, nkv=8, hd=128):
+def read_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
+    d = read_pmc(name)
+    return None if d is None else d.get("traffic_bytes_per_launch")
+
+
+def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label, nkv=8, hd=128, outliers=4):
     """Eager steps (per-kernel events), then the same layer sequence replayed as a HIP graph: the per-layer time is the
     graph's (no host launch cost), the eager one is kept beside it."""
-    lay = Layers(bb, fmt, n_layers, n_keys, rows=rows, nkv=nkv, hd=hd)
+    lay = Layers(bb, fmt, n_layers, n_keys, rows=rows, nkv=nkv, hd=hd, outliers=outliers)
     total_ms, kern, wall = time_layers(bb, ws, lay, steps, warmup)
     eager_us = total_ms * 1e3 / (steps * n_layers)
     g_ms = time_layers_graph(bb, ws, lay, steps, reps=max(1, 64 // n_layers))
@@ -241,15 +298,45 @@ def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label, nkv=8,
         total_ms = g_ms
     per_layer_us = total_ms * 1e3 / (steps * n_layers)
     kmean = float(kern.mean())
-    res = {"workload": label, "us_per_layer": round(per_layer_us, 3), "us_per_layer_eager": round(eager_us, 3),
-           "graph": g_ms is not None, "attn_kernel_us": round(kmean * 1e3, 3),
+    res = {"workload": label, "layers": n_layers, "steps": steps, "us_per_layer": round(per_layer_us, 3),
+           "us_per_layer_eager": round(eager_us, 3), "graph": g_ms is not None, "attn_kernel_us": round(kmean * 1e3, 3),
            "attn_kernel_us_p90": round(float(np.percentile(kern, 90)) * 1e3, 3),
+           "alg_bytes_per_launch": lay.alg_bytes(), "flop_per_launch": lay.flops(),
            "gbs_kernel": round(lay.alg_bytes() / (kmean * 1e-3) / 1e9, 1),
            "gbs_call": round(lay.alg_bytes() / (per_layer_us * 1e-6) / 1e9, 1),
-           "tflops_kernel": round(lay.flops() / (kmean * 1e-3) / 1e12, 2)}
+           "tflops_kernel": round(lay.flops() / (kmean * 1e-3) / 1e12, 2),
+           "tflops_call": round(lay.flops() / (per_layer_us * 1e-6) / 1e12, 2)}
     res["hbm_frac_kernel"] = round(res["gbs_kernel"] / HBM_PEAK_GBS, 4)
     res["mfma_frac_kernel"] = round(res["tflops_kernel"] / FP16_PEAK_TFS, 4)
     return lay, res, total_ms, kern
+
+
+def roofline(res, bound, kernel, pmc_name=None):
+    """The roofline object of a workload's dominant kernel: algorithmic bytes (hbm) or flops (mfma) per launch / its
+    mean duration, against MI355X nameplate; HBM traffic and counters from the committed PMC summary, if any."""
+    if bound == "hbm":
+        ach, peak, unit = res["gbs_kernel"], HBM_PEAK_GBS, "GB/s"
+    else:
+        ach, peak, unit = res["tflops_kernel"], FP16_PEAK_TFS, "TFLOP/s"
+    pmc = read_pmc(pmc_name) if pmc_name else None
+    out = {"bound": bound, "achieved": ach, "peak": peak, "unit": unit, "frac": round(ach / peak, 4),
+           "traffic": pmc.get("traffic_bytes_per_launch") if pmc else None, "kernel": kernel,
+           "kernel_us_mean": res["attn_kernel_us"]}
+    if pmc and pmc.get("counters"):
+        out["counters"] = pmc["counters"]
+    return out
+
+
+def workload(bb, ws, args, key, fmt, n_layers, n_keys, rows, label, bound, kernel, steps, cpu_layers, row_step=1,
+             outliers=4, pmc=None):
+    """One workload: timing, roofline, CPU leg (unless --no-cpu) and the GPU-vs-CPU parity of layer 0."""
+    lay, res, _, _ = run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, 1, label, outliers=outliers)
+    res["roofline"] = roofline(res, bound, kernel, pmc)
+    if not args.no_cpu:
+        res["cpu_baseline"], res["parity_vs_cpu"] = cpu_baseline(bb, lay, min(cpu_layers, n_layers), row_step)
+    lay.close()
+    log(key, json.dumps(res))
+    return res
 
 
 def main():
@@ -258,9 +345,11 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=64)
-    ap.add_argument("--secondary", action="store_true", help="also run the other workloads (4k decode, verify, prefill, q4_0, acceptance)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-layers", type=int, default=64, help="layers of the workload the CPU baseline runs")
+    ap.add_argument("--only", default="", help="comma list of the extra workloads to run (prefill, verify, decode_q4_0, "
+                                                "verify_q4_0, decode_4096, accept); default all")
+    ap.add_argument("--secondary", action="store_true", help="also run the reply side, KV ingest and the head-dim-256 shape")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-layers", type=int, default=16, help="layers of the headline workload the CPU baseline runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "one GPU only: sharding the old pages by position range over several GPUs is a design note, not built",
@@ -273,8 +362,10 @@ def main():
     n_cu = bb.synth().pa_synth_device_name(nb, 64)
     log(f"device {nb.value.decode()} CUs {n_cu}")
     ws = bb.Workspace()
-    bw = measured_copy_bw(bb)
-    log(f"copy {bw['copy']:.0f} GB/s, read {bw['read']:.0f} GB/s")
+    alg = 2 * 131072 * 8 * 136 + 64 * 128 * 4 * 2 + 64 * 8
+    bw = measured_bw(bb, 2 * 131072 * 8 * 136)
+    log(f"copy {bw['copy']:.0f} GB/s, read {bw['read']:.0f} GB/s, one layer per launch {bw['read_layer']:.0f} GB/s "
+        f"({bw['read_layer_us']:.2f} us)")
 
     lay, head, total_ms, kern = run_config(bb, ws, bb.FMT_Q8_0, args.layers, 131072, 8, args.steps, args.warmup,
                                            "decode 1 token x 64 q-heads / 8 kv-heads, hd 128, 131072 q8_0 keys, 64 layers")
@@ -282,50 +373,77 @@ def main():
     cpu, parity = (None, None) if args.no_cpu else cpu_baseline(bb, lay, max(1, min(args.cpu_layers, args.layers)))
     lay.close()
 
+    only = set(x for x in args.only.split(",") if x)
+    want = lambda k: not only or k in only
+    extra = {}
+    nl = args.layers
+    if want("prefill"):
+        extra["prefill"] = workload(
+            bb, ws, args, "prefill", bb.FMT_Q8_0, nl, 65536, 4096,
+            f"prefill chunk: 512 tokens x 64 q-heads / 8 kv-heads (4096 rows per KV head), hd 128, 65536 q8_0 keys, "
+            f"{nl} distinct caches", "mfma", "pa_hip::mma_kernel<1, 8, true, false> (q8_0 prefill)",
+            max(1, min(args.steps, 3)), 1, pmc="prefill", outliers=0)
+    if want("verify"):
+        extra["verify"] = workload(
+            bb, ws, args, "verify", bb.FMT_Q8_0, nl, 98304, 128,
+            f"draft-block verify: 16 tokens x 64 q-heads / 8 kv-heads (128 rows per KV head), hd 128, 98304 q8_0 keys, "
+            f"{nl} layers", "hbm", "pa_hip::mma_kernel<1, 4, true, false> (q8_0 verify)",
+            max(2, min(args.steps, 10)), 4, pmc="verify", outliers=0)
+    if want("decode_q4_0"):
+        extra["decode_q4_0"] = workload(
+            bb, ws, args, "decode_q4_0", bb.FMT_Q4_0, nl, 143360, 8,
+            f"decode 1 token, 8 kv-heads x 8 rows, hd 128, 143360 q4_0 keys, {nl} layers", "hbm",
+            "pa_hip::dec_kernel<2> (q4_0 decode)", args.steps, 16, outliers=0)
+    if want("verify_q4_0"):
+        extra["verify_q4_0"] = workload(
+            bb, ws, args, "verify_q4_0", bb.FMT_Q4_0, nl, 143360, 128,
+            f"verify 16 tokens, 8 kv-heads x 128 rows, hd 128, 143360 q4_0 keys, {nl} layers", "mfma",
+            "pa_hip::mma_kernel<2, 4, true, false> (q4_0 verify)", max(2, min(args.steps, 10)), 2, outliers=0)
+    if want("decode_4096"):
+        extra["decode_4096"] = workload(
+            bb, ws, args, "decode_4096", bb.FMT_Q8_0, 1, 4096, 8,
+            "decode 1 token, 8 kv-heads x 8 rows, hd 128, 4096 q8_0 keys, 1 layer (the ggml-parity workload)", "hbm",
+            "pa_hip::dec_kernel<1> (q8_0 decode)", args.steps, 1, outliers=0)
+    if want("accept"):
+        extra["accept"] = bench_accept(bb, ws, args.steps)
+        log("accept", json.dumps(extra["accept"]))
+
     secondary = []
     if args.secondary:
-        for fmt, nl, nk, rows, nkv, hd, label in (
-                (bb.FMT_Q8_0, 1, 4096, 8, 8, 128, "decode 4096 q8_0 keys (1 layer)"),
-                (bb.FMT_Q8_0, 64, 98304, 128, 8, 128, "verify 16 tokens, 98304 q8_0 keys, 64 layers"),
-                (bb.FMT_Q8_0, 64, 65536, 4096, 8, 128, "prefill 512 tokens, 65536 q8_0 keys, 64 distinct caches"),
-                (bb.FMT_Q4_0, 64, 143360, 8, 8, 128, "decode 143360 q4_0 keys, 64 layers"),
-                (bb.FMT_Q4_0, 64, 143360, 128, 8, 128, "verify 16 tokens, 143360 q4_0 keys, 64 layers"),
-                (bb.FMT_Q8_0, 16, 65536, 48, 4, 256,
-                 "the reference's own shape: 48 rows x 4 KV heads, head dim 256, 65536 q8_0 keys, 16 layers")):
-            st = max(2, min(args.steps, 10)) if rows > 8 else args.steps
-            l2, r2, _, _ = run_config(bb, ws, fmt, nl, nk, rows, st, 1, label, nkv=nkv, hd=hd)
-            l2.close()
-            log("secondary", json.dumps(r2))
-            secondary.append(r2)
-        secondary.append(bench_accept(bb, ws, args.steps))
-        r = bench_reply(bb, ws)
-        log("secondary", json.dumps(r))
-        secondary.append(r)
-        r = bench_ingest(bb)
-        log("secondary", json.dumps(r))
-        secondary.append(r)
+        l2, r2, _, _ = run_config(bb, ws, bb.FMT_Q8_0, 16, 65536, 48, max(2, min(args.steps, 10)), 1,
+                                  "the reference's own shape: 48 rows x 4 KV heads, head dim 256, 65536 q8_0 keys, 16 layers",
+                                  nkv=4, hd=256)
+        l2.close()
+        log("secondary", json.dumps(r2))
+        secondary.append(r2)
+        for fn in (bench_reply, bench_ingest):
+            r = fn(bb, ws) if fn is bench_reply else fn(bb)
+            log("secondary", json.dumps(r))
+            secondary.append(r)
 
-    alg = 2 * 131072 * 8 * 136 + 64 * 128 * 4 * 2 + 64 * 8
     kmean_s = float(kern.mean()) * 1e-3
     achieved = alg / kmean_s / 1e9
     out = {
         "metric": "old-KV attn us/layer + % HBM BW at 128k Q8_0 decode; prefill-chunk TFLOP/s",
         "value": head["us_per_layer"], "unit": "us/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(total_ms / args.steps, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q8_0 K/V, fp16 MFMA, fp32 softmax/accumulate", "data": "synthetic (seeded N(0,1), made on device)",
+        "dtype": "q8_0 K/V; QK int8 MFMA (exact integer block dots), PV fp16 MFMA, fp32 softmax/accumulate",
+        "data": "synthetic (seeded N(0,1), made on device)",
         "config": {"workload": "decode at long context: 1 token, 64 query heads / 8 KV heads (GQA 8), head dim 128, "
                                "131072 old q8_0 positions (32 pages of 4096), K with 4 x8 outlier channels per head",
                    "layers": args.layers, "global_batch": 1, "seq_len": 131072, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode128k"),
                      "kernel": "pa_hip::dec_kernel<1> (q8_0 decode)", "alg_bytes_per_launch": alg,
-                     "kernel_us_mean": round(kmean_s * 1e6, 3)},
+                     "kernel_us_mean": round(kmean_s * 1e6, 3),
+                     "frac_of_read_layer": round(bw["read_layer_us"] / (kmean_s * 1e6), 4)},
         "hbm_frac_call": round(alg / (head["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "timing": {"value_from": "HIP graph of the 64-layer sequence, replayed per step" if head["graph"] else "eager launches",
                    "us_per_layer_eager": head["us_per_layer_eager"], "attn_kernel_us_p90": head["attn_kernel_us_p90"]},
-        "measured_bw_gbs": {k: round(v, 1) for k, v in bw.items()},
+        "measured_bw_gbs": {k: round(v, 1) if k != "read_layer_us" else round(v, 3) for k, v in bw.items()},
         "cpu_baseline": cpu, "parity_vs_cpu": parity,
     }
+    out.update(extra)
     if secondary:
         out["secondary"] = secondary
     print(json.dumps(out), flush=True)

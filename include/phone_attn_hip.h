@@ -85,10 +85,18 @@ typedef struct pa_hip_shape {
 } pa_hip_shape;
 
 /* A workspace: split-K partials and the prepared Q, grown on demand with hipMalloc. Calls that share a workspace must
- * be ordered (same stream, or synchronised); use one workspace per concurrent stream. */
+ * be ordered (same stream, or synchronised); use one workspace per concurrent stream. A buffer that must grow is
+ * replaced, and the old one kept until pa_hip_ws_destroy, so a graph captured earlier stays valid; growth inside a
+ * stream capture is refused (-1): make one eager call of the largest shape before capturing. */
 typedef struct pa_hip_ws pa_hip_ws;
 pa_hip_ws * pa_hip_ws_new(int device);
 void pa_hip_ws_destroy(pa_hip_ws * ws);
+
+/* Split-K geometry of this workspace's calls, for tests and tuning (no counterpart in the reference: the Metal engine
+ * fixes its chunking, pa-metal.mm:627-646). decode_groups > 0: tile groups per head pair and launch of the decode
+ * kernel (<= 8 rows, head dim 128); mma_workgroups > 0: workgroups per launch of the other kernels; 0 restores the
+ * default (about 1024 decode workgroups, one round of resident workgroups otherwise). Returns 0 or -1. */
+int pa_hip_ws_set_split(pa_hip_ws * ws, int decode_groups, int mma_workgroups);
 
 /* engine::alloc_page / free_page (phone-attn.h:168-169): K and V storage of one page in HBM (device pointers, 256-byte
  * aligned). Returns 0 or -1. */

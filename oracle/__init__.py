@@ -49,6 +49,10 @@ def lib() -> C.CDLL:
     L.orc_outlier_channels.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int, vp]
     L.orc_attn_exact.argtypes = [C.POINTER(Shape), vp, vp, vp, i64, vp, vp, vp, C.c_int]
     L.orc_attn_ggml.argtypes = [C.POINTER(Shape), vp, vp, vp, i64, vp, vp, vp, C.c_int]
+    L.orc_attn_ggml_simd.restype = C.c_char_p
+    L.orc_attn_ggml_simd.argtypes = [C.POINTER(Shape), vp, vp, vp, i64, vp, vp, vp, C.c_int, C.c_int]
+    L.orc_simd_path.restype = C.c_char_p
+    L.orc_simd_path.argtypes = []
     L.orc_merge_partial.argtypes = [vp, vp, vp, vp, vp, vp, i64, C.c_int]
     L.orc_normalise.argtypes = [vp, vp, vp, i64, C.c_int, vp, vp]
     L.orc_coattn_merge.argtypes = [vp, vp, vp, vp, vp, i64, C.c_int, vp, vp]
@@ -148,6 +152,23 @@ def attn_ggml(s: Shape, Q: np.ndarray, K: np.ndarray, V: np.ndarray, nk: int, th
     l = np.empty(rows, np.float32)
     lib().orc_attn_ggml(C.byref(s), _p(Q), _p(np.ascontiguousarray(K)), _p(np.ascontiguousarray(V)), nk, _p(O), _p(m), _p(l), threads)
     return O, m, l
+
+
+def attn_ggml_simd(s: Shape, Q: np.ndarray, K: np.ndarray, V: np.ndarray, nk: int, threads: int = 0, level: int = -1):
+    """The CPU baseline: attn_ggml's arithmetic, vectorized (AVX-512 VNNI / AVX2); equal to attn_ggml bit for bit.
+    Returns (O, m, l, simd path)."""
+    rows = s.nkv * s.rows
+    Q = np.ascontiguousarray(Q, np.float32)
+    O = np.empty((rows, s.hd), np.float32)
+    m = np.empty(rows, np.float32)
+    l = np.empty(rows, np.float32)
+    path = lib().orc_attn_ggml_simd(C.byref(s), _p(Q), _p(np.ascontiguousarray(K)), _p(np.ascontiguousarray(V)), nk, _p(O), _p(m),
+                                    _p(l), threads, level)
+    return O, m, l, path.decode()
+
+
+def simd_path() -> str:
+    return lib().orc_simd_path().decode()
 
 
 def merge_partial(O, m, l, O2, m2, l2):

@@ -85,6 +85,15 @@ void orc_attn_exact(const orc_shape * s, const float * Q, const uint8_t * K, con
 void orc_attn_ggml(const orc_shape * s, const float * Q, const uint8_t * K, const uint8_t * V, int64_t nk,
                    float * O, float * m, float * l, int n_threads);
 
+/* The CPU baseline (pa_cpu_simd.c): orc_attn_ggml's arithmetic with ggml's x86 vectorization (AVX-512 VNNI or AVX2
+ * integer block dots, vector dequant and accumulator updates), equal to orc_attn_ggml bit for bit. q8_0 / q4_0 K and V,
+ * ORC_QMODE_GGML, hd a multiple of 32 up to 512 (anything else runs orc_attn_ggml). force_level: -1 = best available,
+ * 2 = AVX-512 VNNI, 1 = AVX2, 0 = scalar. Returns the path taken ("avx512-vnni", "avx2" or "scalar"). */
+const char * orc_attn_ggml_simd(const orc_shape * s, const float * Q, const uint8_t * K, const uint8_t * V, int64_t nk,
+                                float * O, float * m, float * l, int n_threads, int force_level);
+/* the best SIMD path this CPU offers to orc_attn_ggml_simd */
+const char * orc_simd_path(void);
+
 /* merge partial (O2, m2, l2) into (O, m, l), rows of hd (phone-attn.h:231-239) */
 void orc_merge_partial(float * O, float * m, float * l, const float * O2, const float * m2, const float * l2,
                        int64_t rows, int hd);

@@ -38,8 +38,8 @@ def test_committed_traffic_summary():
 
 @pytest.mark.gpu
 def test_bench_json_contract():
-    print("bench --steps 2 --warmup 1 --layers 2 --cpu-layers 1", flush=True)
-    rc, lines, err = run_bench("--steps", "2", "--warmup", "1", "--layers", "2", "--cpu-layers", "1")
+    print("bench --steps 2 --warmup 1 --layers 2 --cpu-layers 1 --only prefill,verify", flush=True)
+    rc, lines, err = run_bench("--steps", "2", "--warmup", "1", "--layers", "2", "--cpu-layers", "1", "--only", "prefill,verify")
     assert rc == 0, err[-2000:]
     assert len(lines) == 1, lines
     out = json.loads(lines[0])
@@ -61,3 +61,16 @@ def test_bench_json_contract():
     assert "orc_attn_ggml" in cb["sample"]
     par = out["parity_vs_cpu"]
     assert par["max_rel_O"] < 2e-3 and par["max_rel_m"] < 2e-3 and par["max_rel_l"] < 2e-3
+    assert cb["simd"] in ("avx512-vnni", "avx2", "scalar") and cb["cpu_model"] and cb["nproc"] >= 1
+    assert out["measured_bw_gbs"]["read_layer"] > 0 and 0 < rf["frac_of_read_layer"] < 1.5
+    assert out["parity_vs_cpu"]["max_rel_O"] < 2e-3
+    # the prefill chunk (the metric's second half) and the verify block, each with its roofline and CPU leg
+    pf, vf = out["prefill"], out["verify"]
+    assert pf["roofline"]["bound"] == "mfma" and pf["roofline"]["unit"] == "TFLOP/s" and pf["roofline"]["peak"] == 2516.6
+    assert pf["roofline"]["achieved"] == pytest.approx(pf["flop_per_launch"] / (pf["attn_kernel_us"] * 1e-6) / 1e12, rel=1e-2)
+    assert 0 < pf["roofline"]["frac"] < 1 and pf["cpu_baseline"]["unit"] == "us/layer"
+    assert "1 layer" in pf["cpu_baseline"]["sample"] or "layers 0..0" in pf["cpu_baseline"]["sample"]
+    assert vf["roofline"]["bound"] == "hbm" and 0 < vf["roofline"]["frac"] < 1
+    assert vf["roofline"]["achieved"] == pytest.approx(vf["alg_bytes_per_launch"] / (vf["attn_kernel_us"] * 1e-6) / 1e9, rel=1e-2)
+    for w in (pf, vf):
+        assert w["parity_vs_cpu"]["max_rel_O"] < 2e-3 and w["parity_vs_cpu"]["max_rel_l"] < 2e-3

@@ -3,8 +3,6 @@
 Tolerance: 2e-3 relative on O (per row, after rebasing to the oracle's max), on m
 (relative to max(1, |m|)) and on l, against the ggml-faithful restatement (orc_attn_ggml) in PA_QMODE_GGML, and against
 the fp64 closed form with the reference engines' rounding (f16(q*scale)) in PA_QMODE_F16."""
-import os
-
 import numpy as np
 import pytest
 
@@ -104,17 +102,15 @@ def test_split_invariance(ws, fmt):
     shape = bb.make_shape(2, 8, 128, fmt, rs=rs)
     ref = orc.attn_ggml(orc.make_shape(2, 8, 128, fmt, orc.QMODE_GGML, rs=rs), Q, K, V, 5000)
     outs = []
-    for env in ({"PA_HIP_GROUPS": "1"}, {"PA_HIP_GROUPS": "3"}, {"PA_HIP_GROUPS": "17"}, {"PA_HIP_GROUPS": "40"},
-                {"PA_HIP_GROUPS": "64"}, {"PA_HIP_GROUPS": "157"}):
-        print("split", env, flush=True)
-        os.environ.update(env)
+    for groups in (1, 3, 17, 40, 64, 157):
+        print("split: decode groups", groups, flush=True)
+        ws.set_split(decode_groups=groups)
         try:
             outs.append(bb.attn_host(shape, K, V, Q, page_keys=1500, ws=ws))
         finally:
-            for k in env:
-                del os.environ[k]
+            ws.set_split()
         eo, em, el = orc.rel_err(*outs[-1], *ref)
-        assert eo < TOL and em < TOL and el < TOL, (env, eo, em, el)
+        assert eo < TOL and em < TOL and el < TOL, (groups, eo, em, el)
     for O, m, l in outs[1:]:
         eo, em, el = orc.rel_err(O, m, l, *outs[0])
         assert eo < 1e-3 and em < 1e-6 and el < 1e-5, (eo, em, el)
@@ -135,14 +131,12 @@ def test_mma_split_invariance(ws, fmt, rows):
     units = nkv * (2 if rows == 512 else 1)                   # KV heads x row blocks (256 rows per block at 512 rows)
     outs = []
     for want in (200, 100, 60, 35, 4, 1):                     # chunks of 1, 2, 3, 5, 40 and 157 tiles
-        env = {"PA_HIP_MMA_TARGET": str(want * units)}
-        print("mma split", env, flush=True)
-        os.environ.update(env)
+        print("mma split: workgroups", want * units, flush=True)
+        ws.set_split(mma_workgroups=want * units)
         try:
             outs.append(bb.attn_host(shape, K, V, Q, page_keys=1500, ws=ws))
         finally:
-            for k in env:
-                del os.environ[k]
+            ws.set_split()
         eo, em, el = orc.rel_err(*outs[-1], *ref)
         assert eo < TOL and em < TOL and el < TOL, (want, eo, em, el)
     for O, m, l in outs[1:]:
@@ -192,8 +186,9 @@ def test_decode_128k_full_size(ws):
 
 @pytest.mark.parametrize("rows", [8, 128])
 def test_page_above_2p20_keys(ws, rows):
-    """One page of 2^20 + 100 keys: the decode path splits it on the host (its per-tile buffer ranges are 32-bit byte
-    counts); the MMA path walks it with 64-bit offsets. Both against the oracle on the same bytes."""
+    """One page of 2^20 + 100 keys, walked in place by the decode path (8 rows) and the matrix-core path (128 rows):
+    each tile's buffer range covers its own 32 rows, so a page of any length needs no split. Both against the oracle
+    on the same bytes."""
     nkv, hd, nk = 2, 128, (1 << 20) + 100
     print(f"page above 2^20 keys rows={rows}", flush=True)
     rs = nkv * bb.head_bytes(bb.FMT_Q8_0, hd)

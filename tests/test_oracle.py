@@ -350,3 +350,23 @@ def test_accept_ties_zeros_nan():
     k, b, am = orc.accept(logits, draft)
     kb, bb, amb = brute_accept(logits, draft)
     assert list(am) == list(amb) == [3, 20, 50] and (k, b) == (kb, bb) == (2, 50)
+
+
+@pytest.mark.parametrize("fmt", [orc.Q8_0, orc.Q4_0])
+@pytest.mark.parametrize("nkv,rows,nk,pad", [(8, 8, 3000, 0), (2, 48, 1000, 16), (1, 5, 777, 0), (3, 130, 500, 8)])
+def test_simd_cpu_baseline_equals_oracle(fmt, nkv, rows, nk, pad):
+    """The vectorized CPU baseline (pa_cpu_simd.c) keeps orc_attn_ggml's operation order: equal bit for bit on every
+    SIMD path this CPU has (outlier keys, padded rows, row counts that are not multiples of the task size)."""
+    hb = orc.head_bytes(fmt, 128)
+    rs = nkv * hb + pad
+    K = orc.fill_rows(61, fmt, nkv, 128, nk, rs=rs, n_outliers=4, outlier_mul=8.0)
+    V = orc.fill_rows(62, fmt, nkv, 128, nk, rs=rs)
+    Q = orc.normal(63, 0, nkv * rows * 128).reshape(-1, 128)
+    s = orc.make_shape(nkv, rows, 128, fmt, rs=rs)
+    ref = orc.attn_ggml(s, Q, K, V, nk)
+    best = orc.simd_path()
+    levels = [1] + ([2] if best == "avx512-vnni" else [])
+    for lv in levels:
+        O, m, l, path = orc.attn_ggml_simd(s, Q, K, V, nk, 0, lv)
+        assert path == ("avx512-vnni" if lv == 2 else "avx2")
+        assert np.array_equal(O, ref[0]) and np.array_equal(m, ref[1]) and np.array_equal(l, ref[2]), path
