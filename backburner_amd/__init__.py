@@ -85,6 +85,8 @@ def lib() -> C.CDLL:
     L.pa_hip_free_page.argtypes = [vp, vp]
     L.pa_hip_attn.restype = C.c_int
     L.pa_hip_attn.argtypes = [vp, C.POINTER(Shape), C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_uint32), C.c_int, vp, vp, vp, vp, vp]
+    L.pa_hip_attn_noalloc.restype = C.c_int
+    L.pa_hip_attn_noalloc.argtypes = [C.POINTER(Shape), C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_uint32), C.c_int, vp, vp, vp, vp, vp]
     L.pa_hip_accept.restype = C.c_int
     L.pa_hip_accept.argtypes = [vp, vp, C.c_int, C.c_int64, vp, vp, vp]
     L.pa_hip_ws_set_split.restype = C.c_int
@@ -316,6 +318,16 @@ class Workspace:
         if self.ptr:
             lib().pa_hip_ws_destroy(self.ptr)
             self.ptr = None
+
+
+def attn_noalloc(shape: Shape, pages: Pages, Q: int, O: int, m: int, l: int, stream=None) -> None:
+    """Enqueue pa_hip_attn_noalloc (no workspace, nothing allocated; the split-K partials use the library's fixed
+    per-GPU scratch)."""
+    n = len(pages.k)
+    kp = (C.c_void_p * max(n, 1))(*pages.k)
+    vp = (C.c_void_p * max(n, 1))(*pages.v)
+    nk = (C.c_uint32 * max(n, 1))(*pages.nkeys)
+    _check(lib().pa_hip_attn_noalloc(C.byref(shape), kp, vp, nk, n, Q, O, m, l, stream), "pa_hip_attn_noalloc")
 
 
 def quantize_device(fmt: int, x: int, y: int, n: int, stream=None) -> None:

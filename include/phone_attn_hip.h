@@ -110,6 +110,17 @@ void pa_hip_free_page(void * k, void * v);
 int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * shape, const void * const * k_pages, const void * const * v_pages,
                 const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, void * stream);
 
+/* No counterpart in the reference: pa_hip_attn for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid hipMalloc). The same arguments without a workspace; the call's split-K partials go
+ * to a fixed device array of PA_HIP_NOALLOC_SCRATCH bytes that each GPU holds from its first such call until the
+ * process ends, and the call allocates nothing. The split adapts so the partials fit (a single launch always does);
+ * a call over more than 64 pages whose launches cannot each hold one split of the rows is refused (-1). Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU race (order them on one stream). Returns 0 once
+ * enqueued, -1 on a bad argument (nothing enqueued). */
+#define PA_HIP_NOALLOC_SCRATCH (64u << 20)
+int pa_hip_attn_noalloc(const pa_hip_shape * shape, const void * const * k_pages, const void * const * v_pages,
+                        const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, void * stream);
+
 /* Greedy acceptance of a draft block (no code in the reference tree: the fork's LLAMA_BATCHED_ARGMAX, serve.sh:8-9, 281):
  * logits fp32 [n_rows][vocab] and draft int32 [n_rows-1] on the device. out (device int32 [2 + n_rows]) receives
  * out[0] = k, the length of the longest prefix with argmax(logits[i]) == draft[i]; out[1] = the bonus token

@@ -1,0 +1,116 @@
+"""pa_hip_attn_noalloc (the engine call that allocates nothing: split-K partials in the library's fixed per-GPU scratch)
+against pa_hip_attn on the same inputs, through the C ABI: two calls in a row, the second smaller (a 16-token verify
+over 98,304 q8_0 keys, then a one-token decode over 4,096 keys), each equal to pa_hip_attn's output bit for bit (the
+same split) and within the 2e-3 parity bar of the oracle; a call over 130 pages (three launches) whose default split
+would overflow the scratch, with the split adapted to fit (within the bar of pa_hip_attn's output and of the oracle);
+and a call whose launches cannot each hold one split, refused with an error before anything is enqueued."""
+import numpy as np
+import pytest
+
+import backburner_amd as bb
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def make(fmt, nkv, rows, nk, seed, page_keys=4096):
+    hb = bb.head_bytes(fmt, 128)
+    rs = nkv * hb
+    syn = bb.synth()
+    kbuf, vbuf = bb.DeviceBuffer(nk * rs), bb.DeviceBuffer(nk * rs)
+    assert syn.pa_synth_fill_rows(kbuf.ptr, fmt, nkv, 128, rs, 0, nk, seed, 1.0, 0, None, 1.0, None) == 0
+    assert syn.pa_synth_fill_rows(vbuf.ptr, fmt, nkv, 128, rs, 0, nk, seed + 1, 1.0, 0, None, 1.0, None) == 0
+    Q = orc.normal(seed + 2, 0, nkv * rows * 128).reshape(-1, 128)
+    sizes = [min(page_keys, nk - i) for i in range(0, nk, page_keys)]
+    pages = bb.Pages([kbuf.ptr + i * rs for i in range(0, nk, page_keys)], [vbuf.ptr + i * rs for i in range(0, nk, page_keys)],
+                     sizes, [])
+    bb.device_sync()
+    return kbuf, vbuf, Q, pages, bb.make_shape(nkv, rows, 128, fmt)
+
+
+def outputs(n, hd=128):
+    return bb.DeviceBuffer(n * hd * 4), bb.DeviceBuffer(n * 8)
+
+
+def read(do, dml, n):
+    ml = dml.download(np.float32)
+    return do.download(np.float32).reshape(n, 128), ml[:n], ml[n:]
+
+
+def both(shape, pages, Q, ws):
+    """(pa_hip_attn_noalloc's (O, m, l), pa_hip_attn's (O, m, l)) on the same inputs"""
+    n = shape.nkv * shape.rows
+    dq = bb.DeviceBuffer.from_array(Q)
+    a, b = outputs(n), outputs(n)
+    try:
+        bb.attn_noalloc(shape, pages, dq.ptr, a[0].ptr, a[1].ptr, a[1].ptr + n * 4)
+        ws.attn(shape, pages, dq.ptr, b[0].ptr, b[1].ptr, b[1].ptr + n * 4)
+        bb.device_sync()
+        return read(*a, n), read(*b, n)
+    finally:
+        for x in (dq, *a, *b):
+            x.close()
+
+
+def test_noalloc_matches_attn_two_calls():
+    ws = bb.Workspace()
+    try:
+        for fmt, nkv, rows, nk, seed in ((bb.FMT_Q8_0, 8, 128, 98304, 7101), (bb.FMT_Q8_0, 8, 8, 4096, 7201)):
+            print(f"noalloc: fmt={fmt} nkv={nkv} rows={rows} nk={nk}", flush=True)
+            kbuf, vbuf, Q, pages, shape = make(fmt, nkv, rows, nk, seed)
+            try:
+                got, want = both(shape, pages, Q, ws)
+                for x, y in zip(got, want):
+                    assert np.array_equal(x, y)                      # the same split: bit for bit
+                sel = np.arange(0, rows, 4 if rows > 8 else 1)
+                idx = (np.arange(nkv)[:, None] * rows + sel[None, :]).reshape(-1)
+                qs = Q.reshape(nkv, rows, 128)[:, sel, :].reshape(-1, 128)
+                ref = orc.attn_ggml(orc.make_shape(nkv, len(sel), 128, fmt), qs, kbuf.download(np.uint8), vbuf.download(np.uint8), nk)
+                eo, em, el = orc.rel_err(got[0][idx], got[1][idx], got[2][idx], *ref)
+                print(f"  vs oracle: O {eo:.2e} m {em:.2e} l {el:.2e}", flush=True)
+                assert eo < TOL and em < TOL and el < TOL
+            finally:
+                kbuf.close(); vbuf.close()
+    finally:
+        ws.close()
+
+
+def test_noalloc_adapts_split_to_scratch():
+    """130 pages of 1,024 keys (three launches of the verify kernel): the default 64 chunks per launch of 128 rows x 8
+    heads would need 102 MB of partials, more than the 64 MiB scratch; the call takes 42 chunks per launch instead."""
+    print("noalloc: 130 pages, verify rows", flush=True)
+    ws = bb.Workspace()
+    kbuf, vbuf, Q, pages, shape = make(bb.FMT_Q8_0, 8, 128, 130 * 1024, 7301, page_keys=1024)
+    try:
+        got, want = both(shape, pages, Q, ws)
+        eo, em, el = orc.rel_err(*got, *want)
+        print(f"  vs pa_hip_attn: O {eo:.2e} m {em:.2e} l {el:.2e}", flush=True)
+        assert eo < TOL and em < TOL and el < TOL
+        sel = np.arange(3, 128, 16)
+        idx = (np.arange(8)[:, None] * 128 + sel[None, :]).reshape(-1)
+        qs = Q.reshape(8, 128, 128)[:, sel, :].reshape(-1, 128)
+        ref = orc.attn_ggml(orc.make_shape(8, len(sel), 128, bb.FMT_Q8_0), qs, kbuf.download(np.uint8), vbuf.download(np.uint8),
+                            130 * 1024)
+        eo, em, el = orc.rel_err(got[0][idx], got[1][idx], got[2][idx], *ref)
+        print(f"  vs oracle: O {eo:.2e} m {em:.2e} l {el:.2e}", flush=True)
+        assert eo < TOL and em < TOL and el < TOL
+    finally:
+        kbuf.close(); vbuf.close(); ws.close()
+
+
+def test_noalloc_refuses_what_cannot_fit():
+    """193 pages (four launches) of 4,096 rows x 8 heads: one split per launch already needs 4 x 17 MB of partials; the
+    host refuses the call before enqueueing anything (the pages are real memory: one 32-key buffer shared by all)."""
+    nkv, rows = 8, 4096
+    rs = nkv * bb.head_bytes(bb.FMT_Q8_0, 128)
+    kv = bb.DeviceBuffer(32 * rs)
+    n = nkv * rows
+    dq, do, dml = bb.DeviceBuffer(n * 128 * 4), bb.DeviceBuffer(n * 128 * 4), bb.DeviceBuffer(n * 8)
+    try:
+        pages = bb.Pages([kv.ptr] * 193, [kv.ptr] * 193, [32] * 193, [])
+        with pytest.raises(bb.PaHipError, match="more slots than the scratch holds"):
+            bb.attn_noalloc(bb.make_shape(nkv, rows, 128, bb.FMT_Q8_0), pages, dq.ptr, do.ptr, dml.ptr, dml.ptr + n * 4)
+    finally:
+        for x in (kv, dq, do, dml):
+            x.close()
