@@ -39,7 +39,9 @@ constexpr int MM_KST = 2 * MM_HD + 16;            // K tile row stride (bytes): 
                                                   // distinct banks
 constexpr int MM_VST = 2 * MM_HD + 64;            // V tile row stride: the 4 rows x 64 bytes of a half-wave's
                                                   // transposing reads hit distinct banks
-constexpr int MM_KT = 32 * MM_KST, MM_VT = 32 * MM_VST, MM_STAGE = MM_KT + MM_VT;
+constexpr int MM_KT = 32 * MM_KST, MM_VT = 32 * MM_VST;
+constexpr int MM_KSC = 32 * 8;                    // exact-QK kernels: the tile's K block scales, [key][4 blocks] fp16
+constexpr int MM_STAGE = MM_KT + MM_VT + MM_KSC;
 constexpr float MM_PMAX = 6.0f;                   // p <= 2^6 between rescales
 constexpr float MM_LOG2E = 1.4426950408889634f;
 
@@ -85,8 +87,8 @@ __device__ __forceinline__ void mm_load_unit_buf(MmRaw<FMT> & r, __amdgpu_buffer
 }
 
 // 16 values -> fp16 (8 dwords). Quantized formats: byte u (unsigned quant) -> fp16 bits 0x6400 | u = 1024 + u exactly,
-// minus (1024 + bias) exactly, times d (one rounding).
-template <int FMT>
+// minus (1024 + bias) exactly, times d (one rounding); with INT the integer quants themselves (exact, no rounding).
+template <int FMT, bool INT = false>
 __device__ __forceinline__ void mm_dequant(const MmRaw<FMT> & r, int half, pa_u4 & lo, pa_u4 & hi) {
     if constexpr (FMT == 0) {
         lo = r.q[0]; hi = r.q[1];
@@ -107,8 +109,13 @@ __device__ __forceinline__ void mm_dequant(const MmRaw<FMT> & r, int half, pa_u4
             const uint32_t x = u[c];
             const mm_h2 a = __builtin_bit_cast(mm_h2, pa_perm(0x64646464u, x, 0x04010400u));   // bytes 0, 1
             const mm_h2 b = __builtin_bit_cast(mm_h2, pa_perm(0x64646464u, x, 0x04030402u));   // bytes 2, 3
-            w[2 * c] = __builtin_bit_cast(uint32_t, (mm_h2) ((a - b2) * d2));
-            w[2 * c + 1] = __builtin_bit_cast(uint32_t, (mm_h2) ((b - b2) * d2));
+            if constexpr (INT) {
+                w[2 * c] = __builtin_bit_cast(uint32_t, (mm_h2) (a - b2));
+                w[2 * c + 1] = __builtin_bit_cast(uint32_t, (mm_h2) (b - b2));
+            } else {
+                w[2 * c] = __builtin_bit_cast(uint32_t, (mm_h2) ((a - b2) * d2));
+                w[2 * c + 1] = __builtin_bit_cast(uint32_t, (mm_h2) ((b - b2) * d2));
+            }
         }
         lo = (pa_u4){w[0], w[1], w[2], w[3]};
         hi = (pa_u4){w[4], w[5], w[6], w[7]};
@@ -155,8 +162,10 @@ struct MmCursor {
 
 // The query rows as the B operand (lane (h2, n) holds row n, dims 16kk + 8h2 + t): PRE -> ggml's q8_0 per 32-block in
 // base-2 units, else f16(q * scale) (or f16(q) for f16 K in PA_QMODE_GGML, ggml's f16 vec_dot type)
-template <int FMT, bool PRE>
-__device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32_t row, bool rlive, int h2, mm_h8 (&Qf)[8]) {
+// EX: the integer quants of ggml's q8_0 (exact in fp16) and the fp16 block scales dqb[b] (bits), for exact block dots.
+template <int FMT, bool PRE, bool EX = false>
+__device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32_t row, bool rlive, int h2, mm_h8 (&Qf)[8],
+                                          uint32_t (&dqb)[4]) {
     const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * MM_HD + 8 * h2;
     const uint32_t qmask = rlive ? 0xffffffffu : 0u;
     pa_f4 x[16];
@@ -182,13 +191,14 @@ __device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             const float dq = (float) (_Float16) d * (scale * MM_LOG2E);   // the fp16 block scale (as ggml stores it)
                                                                           // * scale, in base-2 units
+            dqb[b] = __builtin_bit_cast(uint16_t, (_Float16) d);
             #pragma unroll
             for (int kq = 0; kq < 2; kq++) {
                 mm_h8 f;
                 #pragma unroll
                 for (int t = 0; t < 8; t++) {
                     const float xv = x[4 * b + 2 * kq + t / 4][t % 4];
-                    f[t] = (_Float16) (roundf(xv * id) * dq);
+                    f[t] = EX ? (_Float16) roundf(xv * id) : (_Float16) (roundf(xv * id) * dq);
                 }
                 Qf[2 * b + kq] = f;
             }
@@ -235,12 +245,19 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
 // PRE: PA_QMODE_GGML over quantized K. Q' then carries scale * log2 e inside its one fp16 rounding, and the QK
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
+// EX: exact block dots, as ggml computes them (PRE only). K is staged as its integer quants (exact in fp16) with the
+// block scales beside the tile, Q as its integer quants; per 32-block b the two MFMAs over the block's 32 dims give the
+// integer dot exactly (products below 2^15, sums below 2^24), and one more MFMA gives the exact products
+// dk_b(key) * dq_b(row) of the fp16 block scales (an outer product: the scales in k = 0 of otherwise zero operands).
+// The scores are then sum_b dot_b * dk_b * dq_b in fp32 times scale * log2 e, as ggml's vec_dot does per block,
+// instead of the dot of two fp16-rounded operands.
 // SKIP: a wave whose 32 rows are all past the call's rows only stages (its share of every tile's loads, dequant and LDS
 // stores, and the barriers). For calls with one row block narrower than 32 * NW rows. Without SKIP there is no branch
 // there: one costs 13-20 % on full row blocks, as it separates the next tile's loads from the QK MFMAs, which the
 // compiler otherwise schedules in one basic block.
-template <int FMT, int NW, bool PRE, bool SKIP>
+template <int FMT, int NW, bool PRE, bool SKIP, bool EX>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
+    static_assert(!EX || PRE, "exact block dots need ggml's query rounding over quantized K");
     constexpr int PF = 2;                                            // tiles whose raw bytes are in flight
     constexpr int NT = 64 * NW;
     constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
@@ -297,7 +314,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             const int u = tid + NT * i;
             const int tensor = (wave + NW * i) >> 2, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
             pa_u4 lo, hi;
-            mm_dequant<FMT>(R[i], half, lo, hi);
+            if (EX && tensor == 0) {                                 // K: integer quants, the block scale beside the tile
+                mm_dequant<FMT, true>(R[i], half, lo, hi);
+                if (half == 0) *(uint16_t *) (st + MM_KT + MM_VT + 8 * key + 2 * blk) = (uint16_t) R[i].d;
+            } else {
+                mm_dequant<FMT>(R[i], half, lo, hi);
+            }
             char * dst = tensor ? st + MM_KT + key * MM_VST : st + key * MM_KST;
             dst += 2 * (32 * blk + 16 * half);
             *(pa_u4 *) dst = lo;
@@ -311,7 +333,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     load_tile(R1, t0 + 1, ntiles > 1);
     __builtin_amdgcn_sched_barrier(0);
     mm_h8 Qf[8];
-    mm_prep_q<FMT, PRE>(a, h, row, rlive, h2, Qf);
+    uint32_t dqb[4] = {0u, 0u, 0u, 0u};
+    mm_prep_q<FMT, PRE, EX>(a, h, row, rlive, h2, Qf, dqb);
+    // EX: the B operand of the scale products, dq_b(row n) at k = 0 (lanes h2 = 0), zero elsewhere
+    uint32_t dqw[4];
+    #pragma unroll
+    for (int b = 0; b < 4; b++) dqw[b] = h2 == 0 ? dqb[b] : 0u;
 
     // ---- prologue: tile t0 -> stage 0, tile t0 + 2's loads in flight in R0 (t0 + 1's in R1)
     store_tile(R0, 0);
@@ -323,6 +350,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     for (int db = 0; db < 4; db++) O[db] = (mm_f16){};
     float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
     const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit (!PRE)
+    const float cl2 = a.scale * MM_LOG2E;                             // EX: block-dot sum -> base-2 logit
     mm_f16 Cm = (mm_f16){};                                          // PRE: -mc in every element, the QK start value
     float mc = 0.0f;                                                 // PRE: mref once it is finite (0 before)
     const mm_h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
@@ -338,22 +366,57 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
         // 4(q >> 1) + s / 4, dims 32db + 16(q & 1) + 4(s % 4) .. +3), which complete under the softmax
         __builtin_amdgcn_s_waitcnt(0xc07f);                          // lgkmcnt(0): the stores and any scalar load done,
         mm_h8 kf[8];                                                 // so the MFMAs below wait for their own reads only
-        #pragma unroll
-        for (int kk = 0; kk < 8; kk++) kf[kk] = *(const mm_h8 *) (Kt + n * MM_KST + 32 * kk + 16 * h2);
-        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!EX) {
+            #pragma unroll
+            for (int kk = 0; kk < 8; kk++) kf[kk] = *(const mm_h8 *) (Kt + n * MM_KST + 32 * kk + 16 * h2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         // ---- S^T = K Q'^T, each MFMA followed by the two transposing V reads of one (dim block, key half), so that at
         // most 15 LDS reads are outstanding (the counter's range) and each MFMA waits for its own K read only
-        mm_f16 S = PRE ? Cm : (mm_f16){};
+        mm_f16 S = PRE && !EX ? Cm : (mm_f16){};
         mm_h8 va[4][2];
-        #pragma unroll
-        for (int kk = 0; kk < 8; kk++) {
-            S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], Qf[kk], S, 0, 0, 0);
+        auto v_read = [&](int kk) {
             const int db = kk >> 1, mi = kk & 1;
             const char * vb = Vt + (16 * mi + 4 * (q4 >> 1) + (s4 >> 2)) * MM_VST + 2 * (32 * db + 16 * (q4 & 1) + 4 * (s4 & 3));
             const pa_h4 x0 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) vb));
             const pa_h4 x1 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vb + 8 * MM_VST)));
             va[db][mi] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
-            __builtin_amdgcn_sched_barrier(0);
+        };
+        if constexpr (EX) {
+            // per block: the exact integer dot (two MFMAs), the exact scale products (one MFMA), their fp32 product
+            // summed over the blocks in block order
+            const pa_u2 dk2 = *(const pa_u2 *) (Kt + MM_KT + MM_VT + 8 * n);   // key n's four fp16 block scales
+            const uint32_t hmask = h2 == 0 ? 0xffffffffu : 0u;
+            #pragma unroll
+            for (int kk = 0; kk < 4; kk++) kf[kk] = *(const mm_h8 *) (Kt + n * MM_KST + 32 * kk + 16 * h2);
+            #pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (b < 2) {                                         // the K operands two blocks ahead
+                    kf[4 + 2 * b] = *(const mm_h8 *) (Kt + n * MM_KST + 32 * (4 + 2 * b) + 16 * h2);
+                    kf[5 + 2 * b] = *(const mm_h8 *) (Kt + n * MM_KST + 32 * (5 + 2 * b) + 16 * h2);
+                }
+                mm_f16 Sb = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[2 * b], Qf[2 * b], (mm_f16){}, 0, 0, 0);
+                Sb = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[2 * b + 1], Qf[2 * b + 1], Sb, 0, 0, 0);
+                const uint32_t dkw = ((b & 1) ? dk2[b >> 1] >> 16 : dk2[b >> 1] & 0xffffu) & hmask;
+                const mm_f16 Pb = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mm_h8, (pa_u4){dkw, 0u, 0u, 0u}),
+                                                                         __builtin_bit_cast(mm_h8, (pa_u4){dqw[b], 0u, 0u, 0u}),
+                                                                         (mm_f16){}, 0, 0, 0);
+                #pragma unroll
+                for (int v = 0; v < 16; v++) S[v] = b == 0 ? Pb[v] * Sb[v] : fmaf(Pb[v], Sb[v], S[v]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            #pragma unroll
+            for (int v = 0; v < 16; v++) S[v] = fmaf(S[v], cl2, -mc);  // base-2 logit minus the reference max
+            #pragma unroll
+            for (int kk = 0; kk < 8; kk++) v_read(kk);               // V^T after the block dots (registers), under the
+                                                                     // softmax
+        } else {
+            #pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[kk], Qf[kk], S, 0, 0, 0);
+                v_read(kk);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if (nvalid < 32) {                                           // keys 8j + 4h2 + i past the page's end
             #pragma unroll
@@ -377,8 +440,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
                 #pragma unroll
                 for (int v = 0; v < 16; v++) S[v] -= dl;
                 mc = mn;
-                #pragma unroll
-                for (int v = 0; v < 16; v++) Cm[v] = -mn;
+                if constexpr (!EX) {
+                    #pragma unroll
+                    for (int v = 0; v < 16; v++) Cm[v] = -mn;
+                }
             }
         }
         mx = fmaxf(mx, tm);
@@ -423,17 +488,19 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     mm_write_out(a, O, mref, mx, lsum, h, row, rlive, h2, c);
 }
 
+// Up to 128 rows per KV head (4 waves: verify blocks, short calls) the ggml query rounding takes the exact block dots;
+// prefill chunks (8 waves) take the fp16-operand QK, which the prefill chunk's design specifies (K dequantized to fp16)
 template <int FMT, bool PRE>
 static hipError_t launch_mma_fmt(int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0,
                                  hipEvent_t ev1) {
     switch (nw) {
         case 4:
-            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
-            else hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
+            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, true, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
+            else hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, false, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
             break;
         case 8:
-            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, true>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
-            else hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, false>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, true, false>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            else hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, false, false>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
             break;
         default: return hipErrorInvalidValue;
     }
