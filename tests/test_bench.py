@@ -36,6 +36,22 @@ def test_committed_traffic_summary():
     assert "dec_kernel" in (ROOT / "profiles" / "bench_all_kernels.md").read_text()
 
 
+@pytest.mark.parametrize("name,kernel,flop", [("prefill", "mma_kernel<1, 8, true, false, false>", 4 * 4096 * 65536 * 128 * 8),
+                                              ("verify", "mma_kernel<1, 4, true, false, true>", 4 * 128 * 98304 * 128 * 8)])
+def test_committed_mma_counters(name, kernel, flop):
+    """The matrix-core kernels' counter summaries: the fp16 MFMA work the counters saw (MOPS_F16 x 512) is the
+    algorithmic flops (verify adds its scale-product MFMAs), K/V are fetched about once, and the MFMA busy fraction is
+    derived from the raw cycle counters."""
+    d = json.loads((ROOT / "profiles" / f"{name}_pmc.json").read_text())
+    c = d["counters"]
+    assert kernel in d["kernel"] and d["flop_per_launch"] == flop
+    assert c["fp16_mfma_flops"] == c["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512
+    assert flop <= c["fp16_mfma_flops"] <= 1.3 * flop
+    assert d["alg_bytes_per_launch"] <= d["traffic_bytes_per_launch"] < 1.6 * d["alg_bytes_per_launch"]
+    assert 0 < c["mfma_busy_frac"] < 1 and 0 < c["MfmaUtil_pct"] < 100
+    assert all("rocprofv3 --pmc" in x and "bench.py" in x for x in d["commands"])
+
+
 @pytest.mark.gpu
 def test_bench_json_contract():
     print("bench --steps 2 --warmup 1 --layers 2 --cpu-layers 1 --only prefill,verify", flush=True)
