@@ -102,6 +102,10 @@ def lib() -> C.CDLL:
     L.pa_hip_merge_partial.argtypes = [vp, vp, vp, vp, vp, vp, C.c_uint64, C.c_uint32, vp]
     L.pa_hip_normalise.restype = C.c_int
     L.pa_hip_normalise.argtypes = [vp, vp, vp, C.c_uint64, C.c_uint32, vp, vp, vp]
+    L.pa_hip_pack_q.restype = C.c_int
+    L.pa_hip_pack_q.argtypes = [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]
+    L.pa_hip_unpack_rows.restype = C.c_int
+    L.pa_hip_unpack_rows.argtypes = [vp, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp, vp]
     L.pa_hip_append_rows.restype = C.c_int
     L.pa_hip_append_rows.argtypes = [C.POINTER(Shape), C.POINTER(vp), C.POINTER(vp), C.c_int, C.c_uint32, C.c_uint32, vp, vp,
                                      C.c_uint32, C.c_int, vp]
@@ -340,6 +344,15 @@ def merge_partial_device(O: int, m: int, l: int, O2: int, m2: int, l2: int, rows
 
 def normalise_device(O: int, m: int, l: int, rows: int, hd: int, Oh: int, lse: int, stream=None) -> None:
     _check(lib().pa_hip_normalise(O, m, l, rows, hd, Oh, lse, stream), "pa_hip_normalise")
+
+
+def pack_q_device(qs: int, ng: int, nkv: int, nr: int, hd: int, ntok: int, q: int, stream=None) -> None:
+    _check(lib().pa_hip_pack_q(qs, ng, nkv, nr, hd, ntok, q, stream), "pa_hip_pack_q")
+
+
+def unpack_rows_device(O: int, m: int, l: int, ng: int, nkv: int, nr: int, hd: int, ntok: int, Os: int, ms: int, ls: int,
+                       stream=None) -> None:
+    _check(lib().pa_hip_unpack_rows(O, m, l, ng, nkv, nr, hd, ntok, Os, ms, ls, stream), "pa_hip_unpack_rows")
 
 
 def coattn_merge_device(Oh: int, lse: int, O_loc: int, m_loc: int, l_loc: int, rows: int, hd: int, out: int, lse_out=None,

@@ -38,7 +38,7 @@ SRC_FLAGS = {"pa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-n
 
 LIBS = {
     "libpa_hip.so": ["pa_attn.hip", "pa_decode.hip", "pa_mma.hip", "pa_accept.hip", "pa_reply.hip", "pa_ingest.hip",
-                     "pa_noalloc.hip", "pa_abi.cpp"],
+                     "pa_noalloc.hip", "pa_pack.hip", "pa_abi.cpp"],
     "libpa_synth.so": ["pa_synth.hip"],
 }
 

@@ -1,21 +1,30 @@
 // pa_hip_engine.h - the GPU engine of the reference's phone-attn server on an MI355X: a pa::engine (phone-attn.h:166-183,
 // the interface the Metal engine implements in pa-metal.mm:674-953) over libpa_hip.so's pa_hip_attn.
 //
-// Include phone-attn.h first. One call = one pa_hip_attn launch sequence over the call's pages, on the engine's stream:
-//   begin()  Qs = f16(q*scale) [ng][nkv][NR][HD] -> fp32 [nkv][ng*NR][HD] (exact) in PA_QMODE_F16 with scale 1, the
-//            pages' rows into their HBM copies, the launch, the copy back of (O, m, l); nothing waits
-//   end()    waits, reorders (O, m, l) to the server's [ng][nkv*NR] rows; returns the attention's GPU ms
-// Pages: the unchanged server writes received rows into page.k / page.v with memcpy (store_rows, phone-attn.h:305-319),
-// so they are pinned host memory; page.hk / page.hv are their HBM copies, which begin() refreshes for the rows the
-// call reads (every held row: the engine cannot see a TRUNCATE that rewrites rows in place). A server that stores
-// APPEND rows on the device itself (pa_hip_append_rows) reads the HBM pages with no copy.
+// Include phone-attn.h first. Pages (alloc_page): page.k / page.v are pinned host memory, where the unchanged server
+// stores the rows APPEND receives (store_rows, phone-attn.h:305-319, 418-419); page.hk / page.hv are their copies in HBM,
+// which the kernels read. Each page records how many of its rows the HBM copy holds; a call uploads only the rows past
+// that count, so a steady decode moves only the rows appended since the last call over PCIe, never the held ones.
+// Rows below the count change only after a TRUNCATE (APPEND writes at the held count, phone-attn.h:407): the server
+// reports every TRUNCATE and CONFIG to its page engine (phone-attn.h:344, 395, 437), so this engine registers
+// `row_tracker()` there (server::set_page_engine, phone-attn.h:248); the tracker lowers the counts of the pages past the
+// new end and never takes keys itself (ready() = 0 pages). Without it every call uploads every row it reads.
+//
+// One call (begin) on the engine's stream: the new rows; the f16 queries as they are (pa_hip_pack_q places them as fp32:
+// for one group with ntok_hint < 8 tokens only the 6 x ntok real rows per KV head, pa-metal.mm:630-634, 661-672);
+// pa_hip_attn (PA_QMODE_F16, scale 1: Qs is already f16(q*scale)); pa_hip_unpack_rows into the server's
+// [ng][nkv*NR] rows ((0, -inf, 0) for the tokens the call did not have); one copy back. end() waits and copies
+// (O, m, l) out; it returns the attention's GPU ms.
 // Failure: begin() returns false (the server answers "GPU engine failed to start"); end() returns -1 with
 // O = 0, m = -inf, l = 0, the Metal engine's failure value (pa-metal.mm:932-937).
 #pragma once
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstring>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "phone_attn_hip.h"
@@ -31,6 +40,7 @@ struct hip_engine : pa::engine {
         if (!ws_) return fail(std::string("pa_hip_ws_new: ") + pa_hip_last_error());
         if (hipStreamCreate(&st_) != hipSuccess || hipEventCreate(&e0_) != hipSuccess || hipEventCreate(&e1_) != hipSuccess)
             return fail("stream / events");
+        tracker_.e = this;
         return true;
     }
     ~hip_engine() override {
@@ -43,16 +53,25 @@ struct hip_engine : pa::engine {
         if (st_) (void) hipStreamDestroy(st_);
     }
 
+    // the server's page engine slot: TRUNCATE / CONFIG notices for the uploaded-row counts
+    pa::page_engine * row_tracker() { return &tracker_; }
+
     bool alloc_page(size_t bytes, pa::page & p) override {
         void * k = nullptr, * v = nullptr, * hk = nullptr, * hv = nullptr;
         if (hipHostMalloc(&k, bytes, hipHostMallocDefault) != hipSuccess) return false;
         if (hipHostMalloc(&v, bytes, hipHostMallocDefault) != hipSuccess) { (void) hipHostFree(k); return false; }
         if (pa_hip_alloc_page(bytes, &hk, &hv) != 0) { (void) hipHostFree(k); (void) hipHostFree(v); return false; }
         p.k = (uint8_t *) k; p.v = (uint8_t *) v; p.hk = hk; p.hv = hv;
+        std::lock_guard<std::mutex> lk(mu_);
+        held_[hk] = held();
         return true;
     }
     void free_page(pa::page & p) override {
         (void) hipStreamSynchronize(st_);                            // no copy of this page in flight
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            held_.erase(p.hk);
+        }
         (void) hipHostFree(p.k); (void) hipHostFree(p.v);
         pa_hip_free_page(p.hk, p.hv);
         p = pa::page();
@@ -60,63 +79,49 @@ struct hip_engine : pa::engine {
 
     bool begin(const pa::page * pages, const uint32_t * nkeys, int n_pages, const uint16_t * Qs, const pa::config_req & cfg,
                int ng) override {
-        nkv_ = (int) cfg.n_head_kv; ng_ = ng;
-        const size_t rows = (size_t) ng * nkv_ * pa::NR, qn = rows * pa::HD;
-        const size_t need = (2 * qn + 2 * rows) * sizeof(float);      // device: Q, O, m, l; host: the same
-        if (need > cap_) {
-            (void) hipStreamSynchronize(st_);
-            (void) hipFree(dbuf_); (void) hipHostFree(hbuf_);
-            dbuf_ = nullptr; hbuf_ = nullptr; cap_ = 0;
-            if (hipMalloc((void **) &dbuf_, need) != hipSuccess) return fail("hipMalloc Q/O");
-            if (hipHostMalloc((void **) &hbuf_, need, hipHostMallocDefault) != hipSuccess) return fail("hipHostMalloc Q/O");
-            cap_ = need;
-        }
+        nkv_ = (uint32_t) cfg.n_head_kv; ng_ = (uint32_t) ng;
+        nt_ = (ng == 1 && ntok_hint >= 1 && ntok_hint < 8) ? (uint32_t) ntok_hint : 0;
+        const uint32_t rows = nt_ ? (pa::NR / 8) * nt_ : ng_ * pa::NR;          // call rows per KV head
+        last_rows_ = rows;
+        const size_t srows = (size_t) ng_ * nkv_ * pa::NR, crows = (size_t) nkv_ * rows;
+        // device: qs (f16, server layout) | Q (fp32, call layout) | O, m, l (call) | O, m, l (server); host: qs | O, m, l
+        const size_t qs_b = al(srows * pa::HD * 2), q_b = al(crows * pa::HD * 4), oc_b = al(crows * (pa::HD + 2) * 4);
+        const size_t os_b = al(srows * (pa::HD + 2) * 4);
+        if (!ensure(qs_b + q_b + oc_b + os_b, qs_b + os_b)) return false;
+        if (!upload_rows(pages, nkeys, n_pages, cfg.rs)) return false;
+        char * d = dbuf_;
+        uint16_t * dqs = (uint16_t *) d; float * dq = (float *) (d + qs_b);
+        float * dO = (float *) (d + qs_b + q_b), * dm = dO + crows * pa::HD, * dl = dm + crows;
+        float * sO = (float *) (d + qs_b + q_b + oc_b), * sm = sO + srows * pa::HD, * sl = sm + srows;
+        std::memcpy(hbuf_, Qs, srows * pa::HD * 2);
+        if (hipMemcpyAsync(dqs, hbuf_, srows * pa::HD * 2, hipMemcpyHostToDevice, st_) != hipSuccess) return fail("Q upload");
+        if (pa_hip_pack_q(dqs, ng_, nkv_, pa::NR, pa::HD, nt_, dq, st_) != 0) return fail(std::string("pa_hip_pack_q: ") + pa_hip_last_error());
         std::vector<const void *> kp(n_pages), vp(n_pages);
-        for (int i = 0; i < n_pages; i++) {
-            const size_t b = (size_t) nkeys[i] * cfg.rs;
-            if (hipMemcpyAsync(pages[i].hk, pages[i].k, b, hipMemcpyHostToDevice, st_) != hipSuccess ||
-                hipMemcpyAsync(pages[i].hv, pages[i].v, b, hipMemcpyHostToDevice, st_) != hipSuccess)
-                return fail("page upload");
-            kp[i] = pages[i].hk; vp[i] = pages[i].hv;
-        }
-        float * hq = hbuf_;
-        for (int g = 0; g < ng; g++)                                 // [ng][nkv][NR][HD] -> [nkv][ng*NR][HD]
-            for (int h = 0; h < nkv_; h++)
-                for (int r = 0; r < pa::NR; r++) {
-                    const uint16_t * src = Qs + (((size_t) g * nkv_ + h) * pa::NR + r) * pa::HD;
-                    float * dst = hq + (((size_t) h * ng + g) * pa::NR + r) * pa::HD;
-                    for (int d = 0; d < pa::HD; d++) dst[d] = pa::h2f(src[d]);
-                }
-        float * dq = dbuf_, * dO = dq + qn, * dm = dO + qn, * dl = dm + rows;
-        if (hipMemcpyAsync(dq, hq, qn * sizeof(float), hipMemcpyHostToDevice, st_) != hipSuccess) return fail("Q upload");
-        const pa_hip_shape s = {(uint32_t) nkv_, (uint32_t) (ng * pa::NR), (uint32_t) pa::HD, cfg.is_q8, cfg.rs, cfg.hb,
-                                PA_QMODE_F16, 1.0f};
+        for (int i = 0; i < n_pages; i++) { kp[i] = pages[i].hk; vp[i] = pages[i].hv; }
+        const pa_hip_shape s = {nkv_, rows, (uint32_t) pa::HD, cfg.is_q8, cfg.rs, cfg.hb, PA_QMODE_F16, 1.0f};
         if (hipEventRecord(e0_, st_) != hipSuccess) return fail("event");
         if (pa_hip_attn(ws_, &s, kp.data(), vp.data(), nkeys, n_pages, dq, dO, dm, dl, st_) != 0)
             return fail(std::string("pa_hip_attn: ") + pa_hip_last_error());
-        if (hipEventRecord(e1_, st_) != hipSuccess ||
-            hipMemcpyAsync(hbuf_ + qn, dO, (qn + 2 * rows) * sizeof(float), hipMemcpyDeviceToHost, st_) != hipSuccess)
+        if (hipEventRecord(e1_, st_) != hipSuccess) return fail("event");
+        if (pa_hip_unpack_rows(dO, dm, dl, ng_, nkv_, pa::NR, pa::HD, nt_, sO, sm, sl, st_) != 0)
+            return fail(std::string("pa_hip_unpack_rows: ") + pa_hip_last_error());
+        if (hipMemcpyAsync(hbuf_ + qs_b, sO, srows * (pa::HD + 2) * 4, hipMemcpyDeviceToHost, st_) != hipSuccess)
             return fail("O download");
+        hout_ = (const float *) (hbuf_ + qs_b);
         return true;
     }
 
     double end(float * O, float * m, float * l) override {
-        const size_t rows = (size_t) ng_ * nkv_ * pa::NR, qn = rows * pa::HD;
+        const size_t srows = (size_t) ng_ * nkv_ * pa::NR, qn = srows * pa::HD;
         if (hipStreamSynchronize(st_) != hipSuccess) {
             fail("hipStreamSynchronize");
             for (size_t i = 0; i < qn; i++) O[i] = 0.0f;
-            for (size_t i = 0; i < rows; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
+            for (size_t i = 0; i < srows; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
             return -1.0;
         }
-        const float * hO = hbuf_ + qn, * hm = hO + qn, * hl = hm + rows;
-        for (int g = 0; g < ng_; g++)                                // [nkv][ng*NR] -> [ng][nkv*NR]
-            for (int h = 0; h < nkv_; h++)
-                for (int r = 0; r < pa::NR; r++) {
-                    const size_t src = ((size_t) h * ng_ + g) * pa::NR + r, dst = ((size_t) g * nkv_ + h) * pa::NR + r;
-                    for (int d = 0; d < pa::HD; d++) O[dst * pa::HD + d] = hO[src * pa::HD + d];
-                    m[dst] = hm[src];
-                    l[dst] = hl[src];
-                }
+        std::memcpy(O, hout_, qn * 4);
+        std::memcpy(m, hout_ + qn, srows * 4);
+        std::memcpy(l, hout_ + qn + srows, srows * 4);
         float ms = 0.0f;
         (void) hipEventElapsedTime(&ms, e0_, e1_);
         last_ms_ = ms;
@@ -124,17 +129,83 @@ struct hip_engine : pa::engine {
     }
 
     double exec_ms() const override { return last_ms_; }
-    std::string describe() override { return "hip MI355X (libpa_hip)"; }
+    std::string describe() override {
+        return "hip MI355X (libpa_hip) rows_uploaded=" + std::to_string(rows_up_) + (tracked_ ? " tracked=1" : " tracked=0") +
+               " call_rows_per_kv_head=" + std::to_string(last_rows_);
+    }
+    uint64_t rows_uploaded() const { return rows_up_; }   // K/V rows copied to HBM since init
 
 private:
+    // the page engine the server reports TRUNCATE / CONFIG to; it takes no keys (ready() = 0), builds nothing
+    struct tracker : pa::page_engine {
+        hip_engine * e = nullptr;
+        uint32_t page_keys() const override { return 1u << 31; }        // no page ever completes
+        void configure(const pa::config_req &) override { e->on_configure(); }
+        void queue(uint32_t, uint32_t, const std::vector<pa::page> &) override {}
+        void truncate(uint32_t n) override { e->on_truncate(n); }
+        uint32_t ready(uint32_t, uint32_t) override { return 0; }
+        bool run(uint32_t, uint32_t, const uint16_t *, float *, float *, float *) override { return false; }
+        std::string describe() override { return "hip engine row tracker (no page models)"; }
+    };
+    struct held { uint32_t key0 = 0, rows = 0; bool placed = false; };   // the HBM copy holds rows [0, rows)
+
+    void on_configure() {
+        std::lock_guard<std::mutex> lk(mu_);
+        tracked_ = true;
+        for (auto & x : held_) x.second = held();
+    }
+    void on_truncate(uint32_t n) {
+        std::lock_guard<std::mutex> lk(mu_);
+        for (auto & x : held_) {
+            held & h = x.second;
+            if (h.placed && h.key0 + h.rows > n) h.rows = n > h.key0 ? n - h.key0 : 0;
+        }
+    }
+    // copy rows [held, nkeys) of each page (all rows [0, nkeys) while untracked); the call's pages start at key 0
+    // (the tracker gives no pages to a page engine, so the server's a0 is 0: page i holds keys [i*PAGE, (i+1)*PAGE))
+    bool upload_rows(const pa::page * pages, const uint32_t * nkeys, int n_pages, uint32_t rs) {
+        std::lock_guard<std::mutex> lk(mu_);
+        for (int i = 0; i < n_pages; i++) {
+            held & h = held_[pages[i].hk];
+            h.key0 = (uint32_t) i * pa::PAGE; h.placed = true;
+            const uint32_t from = tracked_ ? std::min(h.rows, nkeys[i]) : 0;
+            if (nkeys[i] > from) {
+                const size_t off = (size_t) from * rs, b = (size_t) (nkeys[i] - from) * rs;
+                if (hipMemcpyAsync((char *) pages[i].hk + off, pages[i].k + off, b, hipMemcpyHostToDevice, st_) != hipSuccess ||
+                    hipMemcpyAsync((char *) pages[i].hv + off, pages[i].v + off, b, hipMemcpyHostToDevice, st_) != hipSuccess)
+                    return fail("page row upload");
+                rows_up_ += nkeys[i] - from;
+            }
+            if (tracked_) h.rows = std::max(h.rows, nkeys[i]);
+        }
+        return true;
+    }
+    static size_t al(size_t b) { return (b + 255) / 256 * 256; }
+    bool ensure(size_t dev_b, size_t host_b) {
+        if (dev_b <= dcap_ && host_b <= hcap_) return true;
+        (void) hipStreamSynchronize(st_);
+        (void) hipFree(dbuf_); (void) hipHostFree(hbuf_);
+        dbuf_ = nullptr; hbuf_ = nullptr; dcap_ = hcap_ = 0;
+        if (hipMalloc((void **) &dbuf_, dev_b) != hipSuccess) return fail("hipMalloc call buffers");
+        if (hipHostMalloc((void **) &hbuf_, host_b, hipHostMallocDefault) != hipSuccess) return fail("hipHostMalloc call buffers");
+        dcap_ = dev_b; hcap_ = host_b;
+        return true;
+    }
     bool fail(const std::string & why) { error = why; return false; }
+
     pa_hip_ws * ws_ = nullptr;
     hipStream_t st_ = nullptr;
     hipEvent_t e0_ = nullptr, e1_ = nullptr;
-    float * dbuf_ = nullptr, * hbuf_ = nullptr;
-    size_t cap_ = 0;
-    int nkv_ = 0, ng_ = 1;
+    char * dbuf_ = nullptr, * hbuf_ = nullptr;
+    size_t dcap_ = 0, hcap_ = 0;
+    const float * hout_ = nullptr;
+    uint32_t nkv_ = 0, ng_ = 1, nt_ = 0, last_rows_ = 0;
     double last_ms_ = 0.0;
+    tracker tracker_;
+    std::mutex mu_;
+    std::unordered_map<void *, held> held_;   // per page (keyed by its HBM K copy)
+    bool tracked_ = false;
+    uint64_t rows_up_ = 0;
 };
 
 }  // namespace pa_hip_server

@@ -23,6 +23,7 @@ int main(int argc, char ** argv) {
     }
     pa::status st;
     pa::server srv(&st, [](const std::string & s) { fprintf(stderr, "%s\n", s.c_str()); }, thr, &eng);
+    srv.set_page_engine(eng.row_tracker());   // TRUNCATE / CONFIG notices: the engine uploads only new rows
     fprintf(stderr, "%s\n", srv.serve(port).c_str());
     return 1;
 }

@@ -181,6 +181,22 @@ int pa_hip_append_f32(const pa_hip_shape * shape, void * const * k_pages, void *
  * PA_QMODE_GGML): n fp32 values (multiple of 32) at x (4-byte aligned) -> blocks at y (2-byte aligned), both device
  * pointers. Returns 0 or -1. */
 int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream);
+/* ---------------------------------------------------------------- 5. The server engine's row layout */
+/* The reference server hands its GPU engine ng groups of query rows (pa::engine::begin, phone-attn.h:174-176): qs =
+ * f16(q*scale) [ng][nkv][nr][hd], row i of a head = GQA member i / 8, token i % 8 (nr a multiple of 8). This places
+ * them, as fp32, in a pa_hip_attn call's Q [nkv][rows][hd] (use PA_QMODE_F16 with scale 1: the values are already
+ * scaled f16): the groups back to back (rows = ng*nr; ntok 0 or 8), or, for one group with 1 <= ntok < 8 real tokens,
+ * only the real rows (rows = (nr/8)*ntok, member k's token t at k*ntok + t), as the Metal engine packs them
+ * (pa::engine::ntok_hint, phone-attn.h:180; pa-metal.mm:630-634, 661-672). Device pointers; qs 8-byte, q 16-byte
+ * aligned; hd a multiple of 4. No counterpart as a function in the reference (its engine packs on the host into shared
+ * memory). Returns 0 once enqueued, -1 on a bad argument. */
+int pa_hip_pack_q(const uint16_t * qs, uint32_t ng, uint32_t nkv, uint32_t nr, uint32_t hd, uint32_t ntok, float * q,
+                  void * stream);
+/* The way back: a call's (O, m, l) [nkv][rows] (rows as pa_hip_pack_q made them) to the server's rows Os [ng][nkv*nr][hd],
+ * ms, ls [ng][nkv*nr]; the rows of tokens the call did not have get (0, -inf, 0), no keys (pa-metal.mm:501-505). Device
+ * pointers, O and Os 16-byte aligned. Returns 0 once enqueued, -1 on a bad argument. */
+int pa_hip_unpack_rows(const float * O, const float * m, const float * l, uint32_t ng, uint32_t nkv, uint32_t nr,
+                       uint32_t hd, uint32_t ntok, float * Os, float * ms, float * ls, void * stream);
 
 #ifdef __cplusplus
 }

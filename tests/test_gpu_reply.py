@@ -180,3 +180,64 @@ def test_reply_pipeline_equals_attention_over_all_keys(ws):
     finally:
         for p in (pa, pb, pall):
             p.close()
+
+
+def server_row_map(ng, nkv, nr, ntok):
+    """The reference Metal engine's row placement (pa-metal.mm:630-634, 661-672; merge: 501-505), restated with plain
+    loops: for each call row (head h, row r) the server row (group g, head h, row i) it comes from, and the call rows
+    per KV head."""
+    nt = ntok if ng == 1 and 1 <= ntok < 8 else 0
+    rows = (nr // 8) * nt if nt else ng * nr
+    src = {}
+    for h in range(nkv):
+        if nt:
+            for k in range(nr // 8):
+                for t in range(nt):
+                    src[(h, k * nt + t)] = (0, h, k * 8 + t)
+        else:
+            for g in range(ng):
+                for i in range(nr):
+                    src[(h, g * nr + i)] = (g, h, i)
+    return rows, src
+
+
+@pytest.mark.parametrize("ng,ntok", [(1, 1), (1, 3), (1, 7), (1, 8), (1, 0), (3, 8)])
+def test_pack_q_and_unpack_rows(ng, ntok):
+    """pa_hip_pack_q / pa_hip_unpack_rows at the reference shape (4 KV heads, 48 rows, hd 256) against the row map
+    above: Q values convert exactly (f16 -> fp32), every call row lands where the map says, and the rows of tokens
+    the call did not have come back as (0, -inf, 0)."""
+    nkv, nr, hd = 4, 48, 256
+    rows, src = server_row_map(ng, nkv, nr, ntok)
+    rng = np.random.default_rng(ng * 10 + ntok)
+    qs = orc.f32_to_f16(rng.standard_normal((ng, nkv, nr, hd)).astype(np.float32))
+    dqs, dq = dev(qs), bb.DeviceBuffer(nkv * rows * hd * 4)
+    bb.pack_q_device(dqs.ptr, ng, nkv, nr, hd, ntok, dq.ptr)
+    bb.device_sync()
+    q = dq.download(np.float32).reshape(nkv, rows, hd)
+    qf = orc.f16_to_f32(qs)
+    for (h, r), (g, hh, i) in src.items():
+        assert np.array_equal(q[h, r], qf[g, hh, i]), (h, r)
+    O = rng.standard_normal((nkv * rows, hd)).astype(np.float32)
+    m = rng.standard_normal(nkv * rows).astype(np.float32)
+    l = rng.uniform(1, 2, nkv * rows).astype(np.float32)
+    dO, dm, dl = dev(O), dev(m), dev(l)
+    sO, sm, sl = bb.DeviceBuffer(ng * nkv * nr * hd * 4), bb.DeviceBuffer(ng * nkv * nr * 4), bb.DeviceBuffer(ng * nkv * nr * 4)
+    bb.unpack_rows_device(dO.ptr, dm.ptr, dl.ptr, ng, nkv, nr, hd, ntok, sO.ptr, sm.ptr, sl.ptr)
+    bb.device_sync()
+    Os = sO.download(np.float32).reshape(ng, nkv, nr, hd)
+    ms, ls = sm.download(np.float32).reshape(ng, nkv, nr), sl.download(np.float32).reshape(ng, nkv, nr)
+    seen = np.zeros((ng, nkv, nr), bool)
+    for (h, r), (g, hh, i) in src.items():
+        assert np.array_equal(Os[g, hh, i], O[h * rows + r]) and ms[g, hh, i] == m[h * rows + r] and ls[g, hh, i] == l[h * rows + r]
+        seen[g, hh, i] = True
+    assert np.all(Os[~seen] == 0) and np.all(np.isneginf(ms[~seen])) and np.all(ls[~seen] == 0)
+    assert seen.sum() == nkv * rows
+    for b in (dqs, dq, dO, dm, dl, sO, sm, sl):
+        b.close()
+
+
+def test_pack_rejects_bad_geometry():
+    with pytest.raises(bb.PaHipError, match="bad geometry"):
+        bb.pack_q_device(0, 2, 4, 48, 256, 3, 0)                 # fewer than 8 tokens needs one group
+    with pytest.raises(bb.PaHipError, match="bad geometry"):
+        bb.unpack_rows_device(0, 0, 0, 1, 4, 44, 256, 8, 0, 0, 0)  # rows per head not a multiple of 8

@@ -1,0 +1,185 @@
+"""The reference's unchanged pa::server over the PATN wire, with the HIP engine (oracle/_ref/pa-hip-serve): pages stay in
+HBM between calls, only appended rows are uploaded, TRUNCATE to the middle of a page followed by APPEND of different
+rows to the same count is seen, and one-group calls with fewer than 8 tokens compute only the real rows.
+
+The client is tests/patn_wire.py. Every reply is checked against the oracle's fp64 attention (orc_attn_exact,
+PA_QMODE_F16: the server's f16(q*scale)) over the rows the layer holds at that moment, as pa-tool's gate does
+(pa-tool.cpp:150-176: max|O - ref| / max|ref| per row and |lse - ref|, PASS below 5e-3; held here to 2e-3). The same
+scenario runs on the CPU against the reference's own server with its C-ABI CPU engine (pa-tool serve linked with
+oracle/sme_cpu.c), which pins the client and the expected values; the GPU run adds the upload counts and the packed
+rows the engine reports in STATS."""
+from __future__ import annotations
+
+import os
+import re
+import socket
+import subprocess
+import time
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from tests.patn_wire import HD, NR, Client
+from tests.test_ref_patool import free_port
+
+ROOT = Path(__file__).resolve().parents[1]
+SERVE_HIP = ROOT / "oracle" / "_ref" / "pa-hip-serve"
+TOOL_CPU = ROOT / "oracle" / "_ref" / "pa-tool-cpu"
+NKV, FMT = 4, orc.Q8_0
+HB = orc.head_bytes(FMT, HD)
+RS = NKV * HB
+SCALE = 1.0 / 16
+TOL = 2e-3
+
+
+class Server:
+    def __init__(self, cmd: list):
+        self.port = free_port()
+        # PA_GPU_MIN_KEYS=0: one-group calls go to the GPU engine below the server's default 16,384 keys too
+        # (phone-attn.h:584-586), so these small layers exercise it
+        env = dict(os.environ, PA_GPU_MIN_KEYS="0")
+        self.p = subprocess.Popen([str(c) for c in cmd] + [str(self.port), "2"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                                  env=env)
+        for _ in range(300):
+            try:
+                socket.create_connection(("127.0.0.1", self.port), timeout=0.2).close()
+                return
+            except OSError:
+                time.sleep(0.1)
+        raise RuntimeError("server did not start")
+
+    def stop(self):
+        self.p.kill()
+        self.p.wait(timeout=30)
+
+
+def rows(seed: int, n: int) -> np.ndarray:
+    return orc.fill_rows(seed, FMT, NKV, HD, n, rs=RS, amp=1.5).reshape(n, RS)
+
+
+def queries(seed: int, ng: int, ntok: int) -> np.ndarray:
+    """f16 bits [ng][nkv][48][256]; rows of tokens >= ntok zero (pa-tool.cpp:126-129)."""
+    q = (orc.normal(seed, 0, ng * NKV * NR * HD) * 1.7).astype(np.float32).reshape(ng, NKV, NR, HD)
+    tok = np.arange(NR) % 8
+    q[:, :, tok >= ntok, :] = 0
+    return orc.f32_to_f16(q).reshape(ng, NKV, NR, HD)
+
+
+def reply_err(O16: np.ndarray, lse: np.ndarray, Q16: np.ndarray, K: np.ndarray, V: np.ndarray, ntok: int, padded_empty: bool):
+    """(max|O - ref|/max|ref|, max|lse - ref|) of every group's reply against the fp64 attention over K/V (the layer's
+    rows); real rows only, as pa-tool."""
+    ng = Q16.shape[0]
+    nk = K.shape[0]
+    eo = el = 0.0
+    for g in range(ng):
+        Qf = orc.f16_to_f32(Q16[g]).reshape(NKV * NR, HD)
+        O, m, l = orc.attn_exact(orc.make_shape(NKV, NR, HD, FMT, orc.QMODE_F16, scale=SCALE, rs=RS), Qf, K, V, nk)
+        ref_o, ref_lse = O / l[:, None], m + np.log(l)
+        got_o = orc.f16_to_f32(O16[g]).reshape(NKV * NR, HD).astype(np.float64)
+        got_lse = lse.reshape(ng, NKV * NR)[g].astype(np.float64)
+        real = (np.arange(NKV * NR) % 8) < ntok
+        den = np.maximum(np.abs(ref_o[real]).max(axis=1), 1e-30)
+        eo = max(eo, float((np.abs(got_o[real] - ref_o[real]).max(axis=1) / den).max()))
+        el = max(el, float(np.abs(got_lse[real] - ref_lse[real]).max()))
+        if padded_empty and ntok < 8:        # tokens the call did not have: no keys -> O = 0, lse = -inf
+            assert np.all(got_o[~real] == 0) and np.all(np.isneginf(got_lse[~real]))
+    return eo, el
+
+
+def check_reply(label, O16, lse, Q16, K, V, ntok, padded_empty):
+    eo, el = reply_err(O16, lse, Q16, K, V, ntok, padded_empty)
+    print(f"{label}: {K.shape[0]} keys, max|O - ref|/max|ref| {eo:.3e}, max|lse - ref| {el:.3e}", flush=True)
+    assert eo < TOL and el < TOL, (label, eo, el)
+
+
+def stat(c: Client, key: str) -> int:
+    m = re.search(key + r"=(\d+)", c.stats())
+    assert m, c.stats()
+    return int(m.group(1))
+
+
+def scenario(cmd: list, ntok: int, gpu: bool):
+    """CONFIG 2 layers; APPEND 6144 keys per layer; ATTN twice; APPEND 64; ATTN; TRUNCATE to 5000 (inside page 1) and
+    APPEND different rows back to 6208; ATTN; TRUNCATE to 3000 (page 1 dropped, inside page 0) and APPEND again;
+    ATTN; then a 16-token ATTN_BIG over the same rows."""
+    srv = Server(cmd)
+    c = Client(srv.port)
+    try:
+        c.hello()
+        c.config(2, NKV, RS, HB, 1)
+        held = rows(11, 6144)
+        for L in range(2):
+            src = held if L == 0 else rows(12, 6144)
+            vs = rows(21 + L, 6144)
+            for p0 in range(0, 6144, 4096):
+                c.append(L, p0, src[p0:p0 + 4096], vs[p0:p0 + 4096])
+            if L == 0:
+                V0 = vs
+        K0 = held
+        Q = queries(31, 1, ntok)
+
+        def attn(label, stale=None):
+            rep, O16, lse = c.attn(0, ntok, 0, SCALE, Q)
+            assert rep["gpu_pages"] == rep["pages"] or not gpu, rep
+            check_reply(f"{label} ntok={ntok}", O16, lse, Q, K0, V0, ntok, gpu)
+            if stale is not None:        # the same reply is far from the rows the TRUNCATE replaced
+                eo, el = reply_err(O16, lse, Q, stale[0], stale[1], ntok, False)
+                assert eo > 50 * TOL, ("the scenario does not tell replaced rows apart", eo, el)
+            return rep
+
+        attn("first call")
+        if gpu:
+            up = stat(c, "rows_uploaded")
+            assert up == 6144 and stat(c, "tracked") == 1
+            assert stat(c, "call_rows_per_kv_head") == (6 * ntok if ntok < 8 else 48)
+        attn("held rows again")
+        if gpu:
+            assert stat(c, "rows_uploaded") == up, "a call over held rows uploaded rows"
+        extra_k, extra_v = rows(41, 64), rows(42, 64)
+        assert c.append(0, 6144, extra_k, extra_v) == 6208
+        K0, V0 = np.concatenate([K0, extra_k]), np.concatenate([V0, extra_v])
+        attn("64 appended rows")
+        if gpu:
+            assert stat(c, "rows_uploaded") == up + 64
+            up += 64
+        for cut, seed in ((5000, 51), (3000, 61)):
+            c.truncate(cut)
+            nk_new = 6208 - cut
+            nk_, nv_ = rows(seed, nk_new), rows(seed + 1, nk_new)
+            for p0 in range(0, nk_new, 2048):
+                assert c.append(0, cut + p0, nk_[p0:p0 + 2048], nv_[p0:p0 + 2048]) == cut + min(nk_new, p0 + 2048)
+            stale = (K0, V0)
+            K0 = np.concatenate([K0[:cut], nk_])
+            V0 = np.concatenate([V0[:cut], nv_])
+            attn(f"TRUNCATE {cut} + APPEND to 6208", stale)
+            if gpu:
+                assert stat(c, "rows_uploaded") == up + nk_new, "not exactly the rewritten rows were uploaded"
+                up += nk_new
+        Qb = queries(71, 2, 8)
+        rep, O16, lse = c.attn(0, 16, 0, SCALE, Qb, big=True)
+        check_reply("ATTN_BIG 16 tokens", O16, lse, Qb, K0, V0, 8, gpu)
+        if gpu:
+            assert stat(c, "rows_uploaded") == up and stat(c, "call_rows_per_kv_head") == 96
+    finally:
+        c.close()
+        srv.stop()
+
+
+needs_cpu_server = pytest.mark.skipif(not TOOL_CPU.exists(), reason="oracle/_ref/pa-tool-cpu not built (reference checkout absent at build time)")
+needs_hip_server = pytest.mark.skipif(not SERVE_HIP.exists(), reason="oracle/_ref/pa-hip-serve not built (reference checkout absent at build time)")
+
+
+@needs_cpu_server
+def test_wire_scenario_on_reference_cpu_server():
+    """The scenario against the reference's server with its CPU engine (no GPU): pins the client and the checks."""
+    scenario([TOOL_CPU, "serve"], 8, gpu=False)
+
+
+@pytest.mark.gpu
+@needs_hip_server
+@pytest.mark.parametrize("ntok", [1, 3, 8])
+def test_wire_scenario_on_hip_engine(ntok):
+    print(f"pa-hip-serve scenario ntok={ntok}", flush=True)
+    scenario([SERVE_HIP], ntok, gpu=True)
