@@ -34,10 +34,10 @@ HIP_FLAGS = [
 #    finite offset; every -inf reference max is tested before it is subtracted), so fmaxf chains need no NaN
 #    canonicalisation: -fno-honor-nans drops those instructions (prefill 3 %, decode 1.5 % faster, measured).
 SRC_FLAGS = {"pa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
-             "pa_mma.hip": ["-fno-honor-nans"]}
+             "pa_mma.hip": ["-fno-honor-nans"], "pa_mma256.hip": ["-fno-honor-nans"]}
 
 LIBS = {
-    "libpa_hip.so": ["pa_attn.hip", "pa_decode.hip", "pa_mma.hip", "pa_accept.hip", "pa_reply.hip", "pa_ingest.hip",
+    "libpa_hip.so": ["pa_attn.hip", "pa_decode.hip", "pa_mma.hip", "pa_mma256.hip", "pa_accept.hip", "pa_reply.hip", "pa_ingest.hip",
                      "pa_noalloc.hip", "pa_pack.hip", "pa_abi.cpp"],
     "libpa_synth.so": ["pa_synth.hip"],
 }

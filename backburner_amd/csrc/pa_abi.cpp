@@ -310,15 +310,18 @@ int attn_decode(Call & cx, const pa_hip_shape * s, const void * const * k_pages,
     return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
 }
 
-// many rows per KV head (verify, prefill; head dim 128): mma_kernel over row blocks of 32*NW rows x chunks of tiles
+// the matrix-core kernels: many rows per KV head at head dim 128 (verify, prefill: mma_kernel, row blocks of 32*NW
+// rows) and fp16-query calls at head dim 256 (mma256_kernel, row blocks of 64 rows), over chunks of 32-key tiles
 int attn_mma(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
              const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
-    // 8 waves above 128 rows (prefill), 4 otherwise (verify, short verify blocks, f16 decode)
-    const uint32_t nw = s->rows > 128 ? 8u : 4u;
-    const uint32_t nrb = (s->rows + 32 * nw - 1) / (32 * nw), qr = nrb * 32 * nw;
+    // head dim 128: 32 rows per wave, 8 waves above 128 rows (prefill), 4 otherwise (verify, short verify blocks, f16
+    // decode); head dim 256: 16 rows per wave, 4 waves (the reference's 48 rows per KV head fill three)
+    const bool h256 = s->hd == 256;
+    const uint32_t nw = h256 ? 4u : s->rows > 128 ? 8u : 4u, rpw = h256 ? 16u : 32u;
+    const uint32_t nrb = (s->rows + rpw * nw - 1) / (rpw * nw), qr = nrb * rpw * nw;
     // one row block with waves past the last row: those waves only stage (with several row blocks the full ones set
     // the time, and the staging-only branch would slow them)
-    const bool skip = nrb == 1 && s->rows <= 32 * (nw - 1);
+    const bool skip = nrb == 1 && s->rows <= rpw * (nw - 1);
     const uint32_t units = s->nkv * nrb;
     const uint64_t rows_per_slot = (uint64_t) s->nkv * qr;
     // key chunks: by default one round of resident workgroups (one of 8 waves or two of 4 per CU, 256 CUs); a second,
@@ -355,8 +358,9 @@ int attn_mma(Call & cx, const pa_hip_shape * s, const void * const * k_pages, co
         a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale; a.s_mul = 1.4426950408889634f;
         a.q = Q; a.po = cx.po; a.pml = cx.pml; a.O = O; a.m = m; a.l = l;
         const uint32_t grid = (a.n_items + 7) / 8 * 8;
-        ok = hip_ok(launch_mma((int) s->fmt, (int) nw, skip, a, grid, st, li == 0 ? cx.ev0 : nullptr,
-                               li + 1 == n_launch ? cx.ev1 : nullptr), "mma launch");
+        hipEvent_t e0 = li == 0 ? cx.ev0 : nullptr, e1 = li + 1 == n_launch ? cx.ev1 : nullptr;
+        ok = hip_ok(h256 ? launch_mma256((int) s->fmt, skip, a, grid, st, e0, e1)
+                         : launch_mma((int) s->fmt, (int) nw, skip, a, grid, st, e0, e1), "mma launch");
         li++;
         slot0 += nch;
     });
@@ -369,7 +373,7 @@ int attn_mma(Call & cx, const pa_hip_shape * s, const void * const * k_pages, co
     return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
 }
 
-// head dim 256 (the reference's compile-time shape): attn_kernel over (key chunk, head, row block) items, chunks of
+// head dim 256 with ggml's q8_0 query rounding: attn_kernel over (key chunk, head, row block) items, chunks of
 // keys that may span pages, about GEN_TARGET_WG workgroups per launch, slot-major slots
 int attn_generic(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
                  const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
@@ -466,6 +470,9 @@ int attn_dispatch(Call & cx, const pa_hip_shape * s, const void * const * k_page
         return attn_decode(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
     // every other head-dim-128 call (verify, prefill, f16 K/V, odd head counts, padded heads)
     if (s->hd == 128) return attn_mma(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
+    // head dim 256 with fp16 queries (the reference engines' f16(q*scale), or f16 K in PA_QMODE_GGML): matrix cores;
+    // ggml's q8_0 query rounding over quantized K at head dim 256 stays on the generic kernel
+    if (s->qmode == PA_QMODE_F16 || s->fmt == PA_FMT_F16) return attn_mma(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
     return attn_generic(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
 }
 

@@ -52,6 +52,8 @@ hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t
                          hipEvent_t ev1 = nullptr);
 hipError_t launch_mma(int fmt, int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
                       hipEvent_t ev1 = nullptr);
+hipError_t launch_mma256(int fmt, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
+                         hipEvent_t ev1 = nullptr);
 hipError_t launch_quantize(int fmt, const float * x, void * y, int64_t n, hipStream_t st);
 
 struct AppendArgs {                 // one page segment of an APPEND: rows j = 0 .. n-1

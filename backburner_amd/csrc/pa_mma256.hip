@@ -1,0 +1,255 @@
+// pa_mma256.hip - partial attention at head dim 256, the reference's compile-time shape (phone-attn.h:78-79: 48 query
+// rows = 8 tokens x GQA 6 per KV head), over q8_0 / q4_0 / f16 K and V on fp16 matrix cores (gfx950). Queries are
+// f16(q*scale) (PA_QMODE_F16, the reference engines' Qs, phone-attn.h:595-599), or f16(q) for f16 K in
+// PA_QMODE_GGML (ggml's f16 vec_dot type; the scale then multiplies the score).
+//
+// One workgroup = one KV head x one block of 64 query rows x one chunk of consecutive 32-key tiles; 4 waves of 16 rows
+// (48 rows: three waves compute, the fourth only stages). Per tile the workgroup dequantizes K and V once into LDS as
+// fp16 (d*q rounded once, as the hd-128 kernel and the Metal engine's dequant, pa-metal.mm:60-66), double-buffered, the
+// next tiles' raw bytes in flight in registers. Each computing wave then runs v_mfma_f32_16x16x32_f16:
+//   S^T (16 keys x 16 rows) = K . Q'^T per 16-key half kh, over 8 steps of 32 dims (Q' stays in registers), so lane
+//   (g, n) holds row n's scores of keys 16kh + 4g + i (i < 4);
+//   O^T (16 dims x 16 rows) += V^T . P^T per dim block (16 blocks), one step over the tile's 32 keys taken in the order
+//   the scores sit in (MFMA k index 8g + 4kh + i = key 16kh + 4g + i): the P operand is the lane's own 8 probabilities,
+//   and V^T comes from two transposing reads (ds_read_b64_tr_b16) per dim block.
+// A row's maximum and sum need the 4 lanes n, n + 16, n + 32, n + 48 (two lane swaps). Online softmax in base 2 with a
+// reference max that moves only when a score exceeds it by more than 2^MM_PMAX (O is rescaled rarely); the exact max is
+// tracked beside it. Output: one split-K slot per workgroup (O unnormalised against the base-2 max, max, sum) or the
+// final (O, m, l) when the call has a single chunk.
+//
+// Reference roles: pa_attn + pa_merge of the Metal engine at this shape (pa-metal.mm:22-131: per (chunk, KV head) a
+// threadgroup of 48 rows dequantizes 32-key K/V blocks into threadgroup memory as half, S = QK^T and O += PV on
+// simdgroup matrices, online softmax, one slot per chunk), and sme_attn_partial's semantics (phone-attn.h:63-65).
+#include "pa_mma.h"
+#include <hip/hip_ext.h>
+
+namespace pa_hip {
+
+constexpr int M2_HD = 256;
+constexpr int M2_KST = 2 * M2_HD + 16;            // K row stride 528 B = 132 dwords: 16 keys' 16-byte reads at one dim
+                                                  // offset hit distinct banks
+constexpr int M2_VST = 2 * M2_HD + 64;            // V row stride 576 B = 144 dwords: a transposing read's 4 rows x
+                                                  // 32 bytes hit distinct banks
+constexpr int M2_KT = 32 * M2_KST, M2_VT = 32 * M2_VST;
+constexpr int M2_STAGE = M2_KT + M2_VT;           // 35,328 B per stage, two stages
+
+// v_permlane16_swap of a value with itself gives every lane the values of lanes l & ~16 and l | 16
+__device__ __forceinline__ float m2_max16(float v) {    // max over lanes l and l ^ 16
+    const auto t = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned) t[0]), __builtin_bit_cast(float, (unsigned) t[1]));
+}
+__device__ __forceinline__ float m2_sum16(float v) {    // sum over lanes l and l ^ 16
+    const auto t = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+    return __builtin_bit_cast(float, (unsigned) t[0]) + __builtin_bit_cast(float, (unsigned) t[1]);
+}
+
+// SKIP: waves whose 16 rows are all past the call's rows only stage (one row block narrower than 64 rows).
+template <int FMT, bool SKIP>
+__global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   // 2 waves per SIMD
+    // NB tiles' raw bytes are in flight while a tile is computed (a ring of NB register buffers); 3 to 5 measured no
+    // faster than 2 at 48 rows x 4 KV heads x 65k q8_0 keys
+    constexpr int NT = 256, NB = 2;
+    constexpr int UPT = 1024 / NT;                                   // staging units per thread (1024 per tile)
+    __shared__ __attribute__((aligned(16))) char smem[2 * M2_STAGE];
+
+    // ---- which (chunk, KV head, row block): row blocks fastest, consecutive items on one XCD (blockIdx % 8 in dispatch
+    // order takes a contiguous item range), so the workgroups sharing a chunk's K/V share its L2
+    const uint32_t bid = blockIdx.x, xcd = bid % 8, local = bid / 8;
+    const uint32_t t8 = (a.n_items + 7) / 8;
+    const uint32_t w = xcd * t8 + local;
+    if (local >= t8 || w >= a.n_items) return;
+    const uint32_t rb = w % a.nrb, h = (w / a.nrb) % a.nkv, c = w / (a.nrb * a.nkv);
+    const uint32_t T = a.cstart[a.n_pages];
+    const uint32_t t0 = c * a.chunk, ntiles = min(t0 + a.chunk, T) - t0;
+
+    const int tid = threadIdx.x, lane = tid % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t row = rb * 64 + 16 * wave + n;
+    const bool rlive = row < a.rows;
+    const bool wlive = !SKIP || rb * 64 + 16 * wave < a.rows;       // uniform: the wave has a live row
+
+    MmCursor cl, cc;
+    cl.init(a); cc.init(a);
+
+    // ---- staging units: u = tid + 256 i -> tensor i >> 1 (uniform), key (u >> 4) & 31, block (u >> 1) & 7, half u & 1
+    using F = MmFmt<FMT>;
+    MmRaw<FMT> R[NB][UPT];                                           // tile j's raw bytes in R[j % NB]
+    auto load_tile = [&](MmRaw<FMT> (&Rb)[UPT], uint32_t tau, bool live) {
+        if (live) cl.seek(a, tau);
+        const uint32_t j0 = live ? 32 * (tau - cl.tb) : 0u;
+        const uint32_t last = live ? cl.nk - 1 - j0 : 0u;
+        const uint32_t nrec = live ? min(last + 1, 32u) * a.rs : 0u;   // the tile's rows only (rs < 2^26)
+        #pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + NT * i;
+            const int tensor = i >> 1, key = (u >> 4) & 31, blk = (u >> 1) & 7, half = u & 1;
+            const uint8_t * base = (tensor ? cl.vb : cl.kb) + (size_t) h * a.hb + (size_t) j0 * a.rs;
+            const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *) base, (short) 0, (int) nrec, 0x00020000);
+            mm_load_unit_buf_al<FMT>(Rb[i], rsrc, min((uint32_t) key, last) * a.rs + blk * F::BB, half,
+                                     (uint32_t) (uintptr_t) base);
+        }
+    };
+    auto store_tile = [&](const MmRaw<FMT> (&Rb)[UPT], int stage) {
+        char * st = smem + stage * M2_STAGE;
+        #pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + NT * i;
+            const int tensor = i >> 1, key = (u >> 4) & 31, blk = (u >> 1) & 7, half = u & 1;
+            pa_u4 lo, hi;
+            mm_dequant<FMT>(Rb[i], half, lo, hi);
+            char * dst = (tensor ? st + M2_KT + key * M2_VST : st + key * M2_KST) + 2 * (32 * blk + 16 * half);
+            *(pa_u4 *) dst = lo;
+            *(pa_u4 *) (dst + 16) = hi;
+        }
+    };
+
+    #pragma unroll
+    for (int i = 0; i < NB; i++) {
+        load_tile(R[i], t0 + i, i == 0 || ntiles > (uint32_t) i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- Q' as the B operand: lane (g, n) holds row n, dims 32 s + 8 g .. +7
+    mm_h8 Qf[8];
+    {
+        const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * M2_HD + 8 * g;
+        const uint32_t qmask = rlive ? 0xffffffffu : 0u;
+        const float qs = a.qmode == 0 ? 1.0f : a.scale;
+        #pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const pa_f4 x0 = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 32 * s)) & qmask);
+            const pa_f4 x1 = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 32 * s + 4)) & qmask);
+            mm_h8 f;
+            #pragma unroll
+            for (int t = 0; t < 4; t++) {
+                f[t] = (_Float16) pa_f32(x0[t] * qs);                // f2h(q * scale)
+                f[t + 4] = (_Float16) pa_f32(x1[t] * qs);
+            }
+            Qf[s] = f;
+        }
+    }
+
+    store_tile(R[0], 0);
+    load_tile(R[0], t0 + NB, ntiles > NB);
+    mm_lds_barrier();
+
+    pa_f4 O[16];
+    #pragma unroll
+    for (int db = 0; db < 16; db++) O[db] = (pa_f4){};
+    float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
+    const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit
+    const mm_h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
+
+    auto compute = [&](int stage, int nvalid) {
+        const char * Kt = smem + stage * M2_STAGE;
+        const char * Vt = Kt + M2_KT;
+        __builtin_amdgcn_s_waitcnt(0xc07f);                          // lgkmcnt(0): the stores and any scalar load done
+        // ---- S^T = K Q'^T: the two key halves' chains interleaved, K read four steps ahead
+        pa_f4 S[2] = {(pa_f4){}, (pa_f4){}};
+        mm_h8 kf[2][4];
+        auto k_read = [&](int s) {
+            #pragma unroll
+            for (int kh = 0; kh < 2; kh++) kf[kh][s & 3] = *(const mm_h8 *) (Kt + (16 * kh + n) * M2_KST + 2 * (32 * s + 8 * g));
+        };
+        #pragma unroll
+        for (int s = 0; s < 4; s++) k_read(s);
+        #pragma unroll
+        for (int s = 0; s < 8; s++) {
+            #pragma unroll
+            for (int kh = 0; kh < 2; kh++) S[kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kh][s & 3], Qf[s], S[kh], 0, 0, 0);
+            if (s + 4 < 8) k_read(s + 4);
+        }
+        if (nvalid < 32) {                                           // keys 16 kh + 4 g + i past the page's end
+            #pragma unroll
+            for (int kh = 0; kh < 2; kh++)
+                #pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (16 * kh + 4 * g + i >= nvalid) S[kh][i] = -INFINITY;
+        }
+        float tm = fmaxf(fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3])), fmaxf(fmaxf(S[1][0], S[1][1]), fmaxf(S[1][2], S[1][3])));
+        tm = mm_max32(m2_max16(tm)) * sm;                            // row n's tile max, base 2
+        if (__builtin_amdgcn_ballot_w64(tm > mref + MM_PMAX)) {
+            const float mn = fmaxf(mref, tm);
+            const float alpha = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mn);
+            #pragma unroll
+            for (int db = 0; db < 16; db++) O[db] *= alpha;
+            lsum *= alpha;
+            mref = mn;
+        }
+        mx = fmaxf(mx, tm);
+        mm_h8 P;
+        #pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+            #pragma unroll
+            for (int i = 0; i < 4; i++) P[4 * kh + i] = (_Float16) __builtin_amdgcn_exp2f(fmaf(S[kh][i], sm, -mref));
+        #pragma unroll
+        for (int t = 0; t < 8; t += 2) {                             // the row sum of the fp16 P the PV MFMAs use
+            const mm_h2 pp = {P[t], P[t + 1]};
+            lsum = __builtin_amdgcn_fdot2(pp, one2, lsum, false);
+        }
+        // ---- O^T += V^T P^T per 16-dim block: lane (g, L) of a transposing read addresses key 16 r + 4 g + L / 4,
+        // dims 16 db + 4 (L % 4) .. +3; lane (g, s) then holds dim 16 db + s of keys 16 r + 4 g + j (j < 4)
+        const char * vrow = Vt + (4 * g + (n >> 2)) * M2_VST + 2 * 4 * (n & 3);
+        #pragma unroll
+        for (int db = 0; db < 16; db++) {
+            const pa_h4 x0 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vrow + 32 * db)));
+            const pa_h4 x1 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vrow + 16 * M2_VST + 32 * db)));
+            const mm_h8 va = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+            O[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, P, O[db], 0, 0, 0);
+        }
+    };
+    auto step = [&](uint32_t t, MmRaw<FMT> (&Rn)[UPT]) {
+        const int stage = t & 1;
+        const uint32_t tau = t0 + t, tn = tau + 1 + NB;              // this tile; the one loaded now
+        cc.seek(a, tau);
+        const int nvalid = (int) min(32u, cc.nk - 32 * (tau - cc.tb));
+        const bool nlive = t + 1 + NB < ntiles;
+        if (nlive) cl.seek(a, tn);
+        store_tile(Rn, stage ^ 1);
+        load_tile(Rn, tn, nlive);
+        if (wlive) compute(stage, nvalid);
+        mm_lds_barrier();
+    };
+    uint32_t t = 0;                                                  // tile t + 1 is in R[(t + 1) % NB]
+    for (; t + NB <= ntiles; t += NB) {
+        #pragma unroll
+        for (int k = 0; k < NB; k++) step(t + k, R[(k + 1) % NB]);
+    }
+    #pragma unroll
+    for (int k = 0; k < NB - 1; k++)
+        if (t + k < ntiles) step(t + k, R[(k + 1) % NB]);
+
+    // ---- row n's result: sum over its 4 lanes, O rebased from the reference max to the exact one
+    const float lt = mm_sum32(m2_sum16(lsum));
+    const float f = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mx);
+    if (!rlive) return;
+    const bool direct = a.n_chunks == 1 && a.fused;
+    float * dst = direct ? a.O + ((size_t) h * a.rows + row) * M2_HD
+                         : a.po + (((size_t) h * a.qr + row) * a.slots + a.slot0 + c) * M2_HD;
+    #pragma unroll
+    for (int db = 0; db < 16; db++) *(pa_f4 *) (dst + 16 * db + 4 * g) = O[db] * f;
+    if (g == 0) {
+        if (direct) {
+            a.m[(size_t) h * a.rows + row] = mx == -INFINITY ? -INFINITY : mx * PA_LN2;
+            a.l[(size_t) h * a.rows + row] = lt * f;
+        } else {
+            a.pml[((size_t) h * a.qr + row) * a.slots + a.slot0 + c] = make_float2(mx, lt * f);
+        }
+    }
+}
+
+hipError_t launch_mma256(int fmt, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    switch (fmt * 2 + (skip ? 1 : 0)) {
+        case 0: hipExtLaunchKernelGGL((mma256_kernel<0, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 1: hipExtLaunchKernelGGL((mma256_kernel<0, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 2: hipExtLaunchKernelGGL((mma256_kernel<1, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 3: hipExtLaunchKernelGGL((mma256_kernel<1, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 4: hipExtLaunchKernelGGL((mma256_kernel<2, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 5: hipExtLaunchKernelGGL((mma256_kernel<2, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace pa_hip

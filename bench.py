@@ -60,7 +60,7 @@ def outlier_channels(seed: int, nkv: int, hd: int, n: int) -> np.ndarray:
 class Layers:
     """n_layers distinct seeded caches: per layer one K slab and one V slab of n_keys rows, viewed as PAGE-key pages."""
 
-    def __init__(self, bb, fmt, n_layers, n_keys, nkv=8, hd=128, rows=8, seed=0x5eed, outliers=4):
+    def __init__(self, bb, fmt, n_layers, n_keys, nkv=8, hd=128, rows=8, seed=0x5eed, outliers=4, qmode=None, scale=None):
         self.bb, self.fmt, self.n_layers, self.n_keys, self.nkv, self.hd, self.rows = bb, fmt, n_layers, n_keys, nkv, hd, rows
         self.hb = bb.head_bytes(fmt, hd)
         self.rs = nkv * self.hb
@@ -89,7 +89,7 @@ class Layers:
         r = nkv * rows
         self.out = bb.DeviceBuffer(r * hd * 4 + 2 * r * 4)
         self.O, self.m, self.l = self.out.ptr, self.out.ptr + r * hd * 4, self.out.ptr + r * hd * 4 + r * 4
-        self.shape = bb.make_shape(nkv, rows, hd, fmt)
+        self.shape = bb.make_shape(nkv, rows, hd, fmt, bb.QMODE_GGML if qmode is None else qmode, scale)
 
     def kv_bytes(self):
         return 2 * self.n_keys * self.rs
@@ -287,10 +287,10 @@ def read_traffic(name: str):
     return None if d is None else d.get("traffic_bytes_per_launch")
 
 
-def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label, nkv=8, hd=128, outliers=4):
+def run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, warmup, label, nkv=8, hd=128, outliers=4, qmode=None, scale=None):
     """Eager steps (per-kernel events), then the same layer sequence replayed as a HIP graph: the per-layer time is the
     graph's (no host launch cost), the eager one is kept beside it."""
-    lay = Layers(bb, fmt, n_layers, n_keys, rows=rows, nkv=nkv, hd=hd, outliers=outliers)
+    lay = Layers(bb, fmt, n_layers, n_keys, rows=rows, nkv=nkv, hd=hd, outliers=outliers, qmode=qmode, scale=scale)
     total_ms, kern, wall = time_layers(bb, ws, lay, steps, warmup)
     eager_us = total_ms * 1e3 / (steps * n_layers)
     g_ms = time_layers_graph(bb, ws, lay, steps, reps=max(1, 64 // n_layers))
@@ -328,11 +328,12 @@ def roofline(res, bound, kernel, pmc_name=None):
 
 
 def workload(bb, ws, args, key, fmt, n_layers, n_keys, rows, label, bound, kernel, steps, cpu_layers, row_step=1,
-             outliers=4, pmc=None):
-    """One workload: timing, roofline, CPU leg (unless --no-cpu) and the GPU-vs-CPU parity of layer 0."""
-    lay, res, _, _ = run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, 1, label, outliers=outliers)
+             outliers=4, pmc=None, **shape):
+    """One workload: timing, roofline, CPU leg (unless --no-cpu or cpu_layers is 0) and the GPU-vs-CPU parity of
+    layer 0. shape: nkv, hd, qmode, scale (default 8 KV heads, head dim 128, ggml's query rounding)."""
+    lay, res, _, _ = run_config(bb, ws, fmt, n_layers, n_keys, rows, steps, 1, label, outliers=outliers, **shape)
     res["roofline"] = roofline(res, bound, kernel, pmc)
-    if not args.no_cpu:
+    if not args.no_cpu and cpu_layers > 0:
         res["cpu_baseline"], res["parity_vs_cpu"] = cpu_baseline(bb, lay, min(cpu_layers, n_layers), row_step)
     lay.close()
     log(key, json.dumps(res))
@@ -346,7 +347,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--only", default="", help="comma list of the extra workloads to run (prefill, verify, decode_q4_0, "
-                                                "verify_q4_0, decode_4096, accept); default all")
+                                                "verify_q4_0, decode_4096, reference_shape, accept); default all")
     ap.add_argument("--secondary", action="store_true", help="also run the reply side, KV ingest and the head-dim-256 shape")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-layers", type=int, default=16, help="layers of the headline workload the CPU baseline runs")
@@ -404,6 +405,12 @@ def main():
             bb, ws, args, "decode_4096", bb.FMT_Q8_0, 1, 4096, 8,
             "decode 1 token, 8 kv-heads x 8 rows, hd 128, 4096 q8_0 keys, 1 layer (the ggml-parity workload)", "hbm",
             "pa_hip::dec_kernel<1> (q8_0 decode)", args.steps, 1, outliers=0)
+    if want("reference_shape"):
+        extra["reference_shape"] = workload(
+            bb, ws, args, "reference_shape", bb.FMT_Q8_0, nl, 65536, 48,
+            f"the reference's own shape: 8 tokens x GQA 6 = 48 rows x 4 KV heads, head dim 256, queries f16(q*scale) "
+            f"(scale 1/16), 65536 q8_0 keys, {nl} layers", "hbm", "pa_hip::mma256_kernel<1, true> (q8_0, head dim 256)",
+            max(2, min(args.steps, 10)), 0, outliers=0, nkv=4, hd=256, qmode=bb.QMODE_F16, scale=1.0 / 16)
     if want("accept"):
         extra["accept"] = bench_accept(bb, ws, args.steps)
         log("accept", json.dumps(extra["accept"]))
@@ -411,8 +418,8 @@ def main():
     secondary = []
     if args.secondary:
         l2, r2, _, _ = run_config(bb, ws, bb.FMT_Q8_0, 16, 65536, 48, max(2, min(args.steps, 10)), 1,
-                                  "the reference's own shape: 48 rows x 4 KV heads, head dim 256, 65536 q8_0 keys, 16 layers",
-                                  nkv=4, hd=256)
+                                  "48 rows x 4 KV heads, head dim 256, 65536 q8_0 keys, 16 layers, ggml's q8_0 query "
+                                  "rounding (the generic head-dim-256 kernel)", nkv=4, hd=256)
         l2.close()
         log("secondary", json.dumps(r2))
         secondary.append(r2)

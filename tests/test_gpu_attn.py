@@ -73,6 +73,39 @@ def test_parity_reference_rounding(ws, fmt, rows):
     run_and_check(ws, fmt, 4, rows, 256, 700, seed=7 + rows + fmt, qmode=bb.QMODE_F16, page_keys=256)
 
 
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16])
+@pytest.mark.parametrize("rows", [6, 16, 18, 48, 64, 96, 150])
+def test_mma256_row_blocks(ws, fmt, rows):
+    """Head dim 256 with fp16 queries (the reference engines' f16(q*scale)) on the matrix-core kernel: 16 rows per wave,
+    64-row blocks. 6 to 48 rows leave one to three waves that only stage, 64 rows none; 96 and 150 rows take several
+    row blocks, the last one partly past the rows."""
+    run_and_check(ws, fmt, 2, rows, 256, 1500, seed=700 + rows + fmt, qmode=bb.QMODE_F16, page_keys=512)
+
+
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_F16])
+def test_mma256_split_invariance(ws, fmt):
+    """The head-dim-256 kernel at the reference's 48 rows x 4 KV heads over chunks of 1, 2, 3, 5 and 40 tiles and one
+    chunk holding all 157 tiles (written directly): each split within the bar of the fp64 form, splits agreeing to the
+    fp16 rounding of P."""
+    nkv, rows, hd, nk = 4, 48, 256, 5000
+    K, V, Q, rs = case(fmt, nkv, rows, hd, nk, 811 + fmt)
+    shape = bb.make_shape(nkv, rows, hd, fmt, bb.QMODE_F16, rs=rs)
+    ref = orc.attn_exact(orc.make_shape(nkv, rows, hd, fmt, orc.QMODE_F16, rs=rs), Q, K, V, nk)
+    outs = []
+    for want in (200, 100, 60, 35, 4, 1):
+        print("mma256 split: workgroups", want * nkv, flush=True)
+        ws.set_split(mma_workgroups=want * nkv)
+        try:
+            outs.append(bb.attn_host(shape, K, V, Q, page_keys=1500, ws=ws))
+        finally:
+            ws.set_split()
+        eo, em, el = orc.rel_err(*outs[-1], *ref)
+        assert eo < TOL and em < TOL and el < TOL, (want, eo, em, el)
+    for O, m, l in outs[1:]:
+        eo, em, el = orc.rel_err(O, m, l, *outs[0])
+        assert eo < 1e-3 and em < 1e-6 and el < 1e-3, (eo, em, el)
+
+
 def test_outlier_channels_and_padding(ws):
     """K with 4 x8 outlier channels per head (the long-context decode configuration) and rows padded past nkv*hb."""
     run_and_check(ws, bb.FMT_Q8_0, 8, 8, 128, 2048, seed=31, rs_pad=16, outliers=4)

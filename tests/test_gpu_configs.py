@@ -10,7 +10,8 @@ O, m and l; orc_attn_ggml in PA_QMODE_GGML):
 - more than 256 split-K slots (a decode over 65 pages: two launches, 272 slots, the generic merge);
 - pages whose byte size exceeds 2^32 (rows of 4,352 bytes, 2^20 + 100 keys), through the decode and the matrix-core
   kernels;
-- head dim 256 calls small enough for a single chunk (the generic kernel writes the result itself).
+- head dim 256 calls small enough for a single chunk (the generic kernel writes the result itself), and the
+  reference's own shape (4 KV heads x 48 rows, head dim 256) at 65,536 keys on the head-dim-256 matrix-core kernel.
 
 Every test prints its errors; the margins are recorded in the design notes."""
 import numpy as np
@@ -183,6 +184,25 @@ def test_hd256_single_chunk(ws, rows, qmode):
             K, V = c.kbuf.download(np.uint8), c.vbuf.download(np.uint8)
             ref = orc.attn_exact(orc.make_shape(2, rows, 256, orc.Q8_0, orc.QMODE_F16, rs=c.rs), c.Q, K, V, 40)
         check(f"hd256 40 keys rows={rows} qmode={qmode}", out, ref)
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("fmt,nk", [(bb.FMT_Q8_0, 65536), (bb.FMT_Q4_0, 65536)])
+def test_reference_shape_full_size(ws, fmt, nk):
+    """The reference's own shape at 65,536 keys: 4 KV heads x 48 rows (8 tokens x GQA 6), head dim 256, queries
+    f16(q*scale) with scale 1/16 (pa-tool's), on the head-dim-256 matrix-core kernel, against the fp64 form."""
+    print(f"reference shape 4 x 48 rows, hd 256, {nk} keys fmt={fmt}", flush=True)
+    c = DevCase(fmt, 4, 48, nk, 4801 + fmt, hd=256)
+    try:
+        shape = bb.make_shape(4, 48, 256, fmt, bb.QMODE_F16, scale=1.0 / 16, rs=c.rs)
+        ws.attn(shape, c.pages, c.dq.ptr, c.do.ptr, c.dml.ptr, c.dml.ptr + 4 * 48 * 4)
+        bb.device_sync()
+        ml = c.dml.download(np.float32)
+        out = c.do.download(np.float32).reshape(4 * 48, 256), ml[:192], ml[192:]
+        K, V = c.kbuf.download(np.uint8), c.vbuf.download(np.uint8)
+        ref = orc.attn_exact(orc.make_shape(4, 48, 256, fmt, orc.QMODE_F16, scale=1.0 / 16, rs=c.rs), c.Q, K, V, nk)
+        check(f"reference shape {nk} fmt={fmt}", out, ref)
     finally:
         c.close()
 
