@@ -1,17 +1,27 @@
 // pa_hip_serve.cpp - the reference's phone-attn server on Linux with the HIP engine: pa::server (phone-attn.h:241-739,
 // unchanged) constructed with a pa_hip_server::hip_engine, as pa-tool's `serve` mode constructs it with the Metal engine
-// (pa-tool.cpp:54-68). The unchanged pa-tool client (`pa-tool test HOST PORT ... gpu_permille=1000`) then drives the
-// GPU over the PATN wire: CONFIG, APPEND into the engine's pages, ATTN / ATTN_BIG, TRUNCATE, STATS.
+// (pa-tool.cpp:54-68), and the engine's row tracker in the server's page-engine slot (its TRUNCATE / CONFIG notices). The
+// unchanged pa-tool client (`pa-tool test HOST PORT ... gpu_permille=1000`) then drives the GPU over the PATN wire:
+// CONFIG, APPEND into the engine's pages, ATTN / ATTN_BIG, TRUNCATE, STATS.
 //
 //   pa-hip-serve [port] [threads]
 //
-// Built by oracle/Makefile where the reference checkout (phone-attn.h) is present; the server's non-GPU pages go to the
-// sme_* C ABI, which libpa_hip.so also exports.
+// SIGTERM / SIGINT end the process with a normal exit (exit handlers run, so a profiler wrapping the server writes its
+// results); send it between sessions. Built by oracle/Makefile where the reference checkout (phone-attn.h) is present;
+// the server's non-GPU pages go to the sme_* C ABI, which libpa_hip.so also exports.
 #include "phone-attn.h"
 #include "pa_hip_engine.h"
 
+#include <atomic>
+#include <chrono>
+#include <csignal>
 #include <cstdio>
 #include <cstdlib>
+#include <thread>
+
+static std::atomic<int> g_stop{0};   // 1: a signal asked to stop; 2: the server loop ended
+
+static void on_signal(int) { g_stop.store(1); }
 
 int main(int argc, char ** argv) {
     const int port = argc > 1 ? atoi(argv[1]) : pa::DEFAULT_PORT;
@@ -24,6 +34,12 @@ int main(int argc, char ** argv) {
     pa::status st;
     pa::server srv(&st, [](const std::string & s) { fprintf(stderr, "%s\n", s.c_str()); }, thr, &eng);
     srv.set_page_engine(eng.row_tracker());   // TRUNCATE / CONFIG notices: the engine uploads only new rows
-    fprintf(stderr, "%s\n", srv.serve(port).c_str());
-    return 1;
+    std::signal(SIGTERM, on_signal);
+    std::signal(SIGINT, on_signal);
+    std::thread([&] {
+        fprintf(stderr, "%s\n", srv.serve(port).c_str());
+        g_stop.store(2);
+    }).detach();
+    while (g_stop.load() == 0) std::this_thread::sleep_for(std::chrono::milliseconds(20));
+    std::exit(g_stop.load() == 2 ? 1 : 0);   // the serving thread stays blocked in accept()
 }

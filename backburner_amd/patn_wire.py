@@ -1,7 +1,7 @@
-"""A PATN wire client for tests: the message layout of phone-attn.h:74-94 (hdr, config_req, append_req, attn_req,
-attn_rep; message numbers of the `msg` enum) and the calls of the reference client (phone-attn.h:755-785), restated in
-Python so a test can send CONFIG / APPEND / TRUNCATE / ATTN / ATTN_BIG / STATS in any order. Test infrastructure: the
-product never imports it."""
+"""A PATN wire client (the Mac side of the link, in Python): the message layout of phone-attn.h:74-94 (hdr,
+config_req, append_req, attn_req, attn_rep; message numbers of the `msg` enum) and the calls of the reference client
+(phone-attn.h:755-785), restated in Python, so a test or a probe can send CONFIG / APPEND / TRUNCATE / ATTN / ATTN_BIG / STATS in any order to a server
+such as pa-hip-serve. Pure Python (sockets and numpy); nothing here touches the GPU."""
 from __future__ import annotations
 
 import socket

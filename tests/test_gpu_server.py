@@ -2,7 +2,7 @@
 HBM between calls, only appended rows are uploaded, TRUNCATE to the middle of a page followed by APPEND of different
 rows to the same count is seen, and one-group calls with fewer than 8 tokens compute only the real rows.
 
-The client is tests/patn_wire.py. Every reply is checked against the oracle's fp64 attention (orc_attn_exact,
+The client is backburner_amd/patn_wire.py. Every reply is checked against the oracle's fp64 attention (orc_attn_exact,
 PA_QMODE_F16: the server's f16(q*scale)) over the rows the layer holds at that moment, as pa-tool's gate does
 (pa-tool.cpp:150-176: max|O - ref| / max|ref| per row and |lse - ref|, PASS below 5e-3; held here to 2e-3). The same
 scenario runs on the CPU against the reference's own server with its C-ABI CPU engine (pa-tool serve linked with
@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from tests.patn_wire import HD, NR, Client
+from backburner_amd.patn_wire import HD, NR, Client
 from tests.test_ref_patool import free_port
 
 ROOT = Path(__file__).resolve().parents[1]
