@@ -133,10 +133,11 @@ extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
 extern "C" void pa_hip_ws_destroy(pa_hip_ws * w) {
     if (!w) return;
     (void) hipDeviceSynchronize();
-    hipFree(w->po); hipFree(w->pml); hipFree(w->apart); hipFree(w->acount);
-    hipFree(w->dk); hipFree(w->dv); hipFree(w->dq); hipFree(w->dout); hipFree(w->ro); hipFree(w->rml);
-    for (void * p : w->retired) hipFree(p);
-    if (w->stream) hipStreamDestroy(w->stream);
+    for (void * p : {(void *) w->po, (void *) w->pml, (void *) w->apart, (void *) w->acount, (void *) w->dk,
+                     (void *) w->dv, (void *) w->dq, (void *) w->dout, (void *) w->ro, (void *) w->rml})
+        (void) hipFree(p);
+    for (void * p : w->retired) (void) hipFree(p);
+    if (w->stream) (void) hipStreamDestroy(w->stream);
     delete w;
 }
 
@@ -160,13 +161,13 @@ extern "C" int pa_hip_alloc_page(size_t bytes, void ** k, void ** v) {
     *k = *v = nullptr;
     if (!device_usable()) { set_err("pa_hip_alloc_page: " + g_dev_why); return -1; }
     if (!hip_ok(hipMalloc(k, bytes), "hipMalloc page K")) return -1;
-    if (!hip_ok(hipMalloc(v, bytes), "hipMalloc page V")) { hipFree(*k); *k = nullptr; return -1; }
+    if (!hip_ok(hipMalloc(v, bytes), "hipMalloc page V")) { (void) hipFree(*k); *k = nullptr; return -1; }
     return 0;
 }
 
 extern "C" void pa_hip_free_page(void * k, void * v) {
-    if (k) hipFree(k);
-    if (v) hipFree(v);
+    if (k) (void) hipFree(k);
+    if (v) (void) hipFree(v);
 }
 
 // ---------------------------------------------------------------- the engine path

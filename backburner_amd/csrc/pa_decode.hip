@@ -43,7 +43,6 @@ typedef __fp16 dec_h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 #define DEC_LDS __attribute__((address_space(3)))
 
 constexpr int DEC_HD = 128;
-constexpr int DEC_QR = 8;                 // rows per KV head in the split-K slots
 constexpr int DEC_NKB = DEC_HD / 32;      // quant blocks per head row
 constexpr int DEC_ND = DEC_HD / 16;       // 16-dim blocks of O^T
 constexpr int DEC_VST = DEC_HD + 16;      // LDS bytes per V tile row (16 bytes of padding: conflict-free tr_b8 reads)

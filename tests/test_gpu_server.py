@@ -183,3 +183,33 @@ def test_wire_scenario_on_reference_cpu_server():
 def test_wire_scenario_on_hip_engine(ntok):
     print(f"pa-hip-serve scenario ntok={ntok}", flush=True)
     scenario([SERVE_HIP], ntok, gpu=True)
+
+
+def run_probe(server: Path, keys: int, calls: int) -> dict:
+    import json
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "backburner_amd" / "integration" / "serve_probe.py"), "--server", str(server),
+                        "--keys", str(keys), "--calls", str(calls)], capture_output=True, text=True, timeout=300,
+                       env=dict(os.environ, PA_GPU_MIN_KEYS="0"))
+    assert r.returncode == 0, r.stdout + r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+@needs_cpu_server
+def test_serve_probe_on_reference_cpu_server():
+    """The server probe's wire sequence against the reference's server with its CPU engine (no GPU): one JSON line
+    with both timed phases; that server has no HIP engine, so no upload counts."""
+    out = run_probe(TOOL_CPU, 4096, 2)
+    assert out["held"]["calls"] == 2 and out["append64"]["calls"] == 2
+    assert out["rows_uploaded_per_held_call"] is None
+
+
+@pytest.mark.gpu
+@needs_hip_server
+def test_serve_probe_on_hip_engine():
+    """The server probe through pa-hip-serve: calls over held rows upload nothing, a 64-row APPEND uploads 64 rows."""
+    print("serve probe, 8192 keys", flush=True)
+    out = run_probe(SERVE_HIP, 8192, 4)
+    assert out["rows_uploaded"]["after_warmup"] == 8192
+    assert out["rows_uploaded_per_held_call"] == 0 and out["rows_uploaded_per_append_call"] == 64
+    assert out["held"]["gpu_ms_p50"] > 0
