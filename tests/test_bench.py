@@ -37,7 +37,8 @@ def test_committed_traffic_summary():
 
 
 @pytest.mark.parametrize("name,kernel,flop", [("prefill", "mma_kernel<1, 8, true, false, false>", 4 * 4096 * 65536 * 128 * 8),
-                                              ("verify", "mma_kernel<1, 4, true, false, true>", 4 * 128 * 98304 * 128 * 8)])
+                                              ("verify", "mma_kernel<1, 4, true, false, true>", 4 * 128 * 98304 * 128 * 8),
+                                              ("reference_shape", "mma256_kernel<1, true>", 4 * 48 * 65536 * 256 * 4)])
 def test_committed_mma_counters(name, kernel, flop):
     """The matrix-core kernels' counter summaries: the fp16 MFMA work the counters saw (MOPS_F16 x 512) is the
     algorithmic flops (verify adds its scale-product MFMAs), K/V are fetched about once, and the MFMA busy fraction is
