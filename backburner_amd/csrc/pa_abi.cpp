@@ -173,7 +173,10 @@ extern "C" void pa_hip_free_page(void * k, void * v) {
 // ---------------------------------------------------------------- the engine path
 namespace {
 
-constexpr int DEC_TARGET_WG = 1024;   // decode workgroups per launch: four of two waves per CU
+// decode workgroups per launch (two waves each). q8_0: three per CU, one round (at 8 KV heads x 128k keys 56.4-57.0 us
+// per layer against 58.3-58.4 at four per CU; 64k and 256k keys alike; counts between them leave a partial second
+// round and are slower). q4_0, twice the work per byte: four per CU (45.4-46.4 against 49.5-50.2 us at three).
+constexpr int DEC_TARGET_WG_Q8 = 768, DEC_TARGET_WG_Q4 = 1024;
 constexpr int GEN_TARGET_WG = 256;    // head dim 256 kernel: one round of resident workgroups
 
 // One call of the engine path: where its split-K slots go, its geometry overrides, its timing events and, for
@@ -256,8 +259,8 @@ uint64_t chunk_cap(const Call & cx, uint32_t n_launch, uint64_t rows_per_chunk, 
 }
 
 // decode calls (<= 8 rows per KV head, q8_0 / q4_0, ggml query rounding, head_dim 128): dec_kernel over (tile group,
-// head pair) items - group c of G takes the launch's 32-key tiles c, c + G, ... - about DEC_TARGET_WG workgroups per
-// launch, then the merge kernel
+// head pair) items - group c of G takes the launch's 32-key tiles c, c + G, ... - about DEC_TARGET_WG_Q8 / _Q4
+// workgroups per launch, then the merge kernel
 int attn_decode(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
                 const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
     const uint32_t qr = 8;
@@ -265,8 +268,9 @@ int attn_decode(Call & cx, const pa_hip_shape * s, const void * const * k_pages,
     // tile groups per head pair: at least two tiles per group unless forced (one-tile groups leave each workgroup's
     // first-load latency and slot write unhidden: 4096 keys 9.7 us at 256 workgroups against 11.8 us at 512)
     auto groups = [&](uint64_t tiles, uint64_t cap) {
+        const uint64_t target = s->fmt == PA_FMT_Q4_0 ? DEC_TARGET_WG_Q4 : DEC_TARGET_WG_Q8;
         const uint64_t want = cx.dec_groups > 0 ? (uint64_t) cx.dec_groups
-                                                : std::min<uint64_t>(std::max<uint64_t>(1, DEC_TARGET_WG / (s->nkv / 2)), (tiles + 1) / 2);
+                                                : std::min<uint64_t>(std::max<uint64_t>(1, target / (s->nkv / 2)), (tiles + 1) / 2);
         return (uint32_t) std::max<uint64_t>(1, std::min({tiles, want, cap}));
     };
     uint32_t n_launch = 0;

@@ -144,12 +144,18 @@ def test_verify_full_size_outlier_keys(ws, fmt, nk):
 
 @pytest.mark.parametrize("rows", [8, 128])
 def test_more_than_256_slots(ws, rows):
-    """65 pages of 1,024 keys: two launches. Decode: 256 + 16 tile groups = 272 split-K slots per row (the generic merge
-    kernel); verify: 64 + 32 chunks (the wide merge over 96 slots)."""
+    """65 pages of 1,024 keys: two launches. Decode with 256 tile groups per head pair (the q4_0 default; set here for
+    q8_0): 256 + 16 = 272 split-K slots per row (the generic merge kernel); verify: 64 + 32 chunks (the wide merge over
+    96 slots)."""
     print(f"65 pages, rows={rows}", flush=True)
     c = DevCase(bb.FMT_Q8_0, 8, rows, 65 * 1024, 4401 + rows, page_keys=1024)
     try:
-        out = c.run(ws)
+        if rows == 8:
+            ws.set_split(decode_groups=256)
+        try:
+            out = c.run(ws)
+        finally:
+            ws.set_split()
         sel = np.arange(rows) if rows == 8 else np.arange(1, rows, 8)
         check(f"65 pages rows={rows}", pick(out, 8, rows, sel), c.oracle(sel))
     finally:
