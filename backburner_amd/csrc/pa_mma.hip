@@ -38,7 +38,10 @@ constexpr int MM_STAGE = MM_KT + MM_VT + MM_KSC;
 
 // The query rows as the B operand (lane (h2, n) holds row n, dims 16kk + 8h2 + t): PRE -> ggml's q8_0 per 32-block in
 // base-2 units, else f16(q * scale) (or f16(q) for f16 K in PA_QMODE_GGML, ggml's f16 vec_dot type)
-// EX: the integer quants of ggml's q8_0 (exact in fp16) and the fp16 block scales dqb[b] (bits), for exact block dots.
+// EX: for exact block dots, ggml's q8_0 integer quants times 2^-s_b (exact in fp16) and, per block, the pair
+// (hi, lo) of fp16 values whose sum is the fp16 block scale times scale * log2 e * 2^s_b to about 22 bits (dqb[b]:
+// hi in the low half). s_b puts that product in [8, 16), so neither half overflows or loses bits to subnormals (capped
+// at 14, where the quants' 2^-s_b stays normal).
 template <int FMT, bool PRE, bool EX = false>
 __device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32_t row, bool rlive, int h2, mm_h8 (&Qf)[8],
                                           uint32_t (&dqb)[4]) {
@@ -67,14 +70,20 @@ __device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             const float dq = (float) (_Float16) d * (scale * MM_LOG2E);   // the fp16 block scale (as ggml stores it)
                                                                           // * scale, in base-2 units
-            dqb[b] = __builtin_bit_cast(uint16_t, (_Float16) d);
+            int sb = 0;
+            if constexpr (EX) {
+                sb = dq > 0.0f ? min(14, 3 - __builtin_amdgcn_frexp_expf(dq) + 1) : 0;   // dq * 2^sb in [8, 16)
+                const float v = __builtin_amdgcn_ldexpf(dq, sb);
+                const _Float16 hi = (_Float16) v, lo = (_Float16) (v - (float) hi);
+                dqb[b] = (uint32_t) __builtin_bit_cast(uint16_t, hi) | ((uint32_t) __builtin_bit_cast(uint16_t, lo) << 16);
+            }
             #pragma unroll
             for (int kq = 0; kq < 2; kq++) {
                 mm_h8 f;
                 #pragma unroll
                 for (int t = 0; t < 8; t++) {
                     const float xv = x[4 * b + 2 * kq + t / 4][t % 4];
-                    f[t] = EX ? (_Float16) roundf(xv * id) : (_Float16) (roundf(xv * id) * dq);
+                    f[t] = EX ? (_Float16) __builtin_amdgcn_ldexpf(roundf(xv * id), -sb) : (_Float16) (roundf(xv * id) * dq);
                 }
                 Qf[2 * b + kq] = f;
             }
@@ -122,11 +131,12 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
 // EX: exact block dots, as ggml computes them (PRE only). K is staged as its integer quants (exact in fp16) with the
-// block scales beside the tile, Q as its integer quants; per 32-block b the two MFMAs over the block's 32 dims give the
-// integer dot exactly (products below 2^15, sums below 2^24), and one more MFMA gives the exact products
-// dk_b(key) * dq_b(row) of the fp16 block scales (an outer product: the scales in k = 0 of otherwise zero operands).
-// The scores are then sum_b dot_b * dk_b * dq_b in fp32 times scale * log2 e, as ggml's vec_dot does per block,
-// instead of the dot of two fp16-rounded operands.
+// block scales beside the tile, Q as its integer quants times 2^-s_b; per 32-block b the two MFMAs over the block's 32
+// dims give the integer dot times 2^-s_b exactly (products below 2^15, sums below 2^24), and one more MFMA gives
+// dk_b(key) * (hi + lo)(row): dk_b at k = 0 and 1 of A, the row's pair at k = 0 and 1 of B (an outer product in
+// otherwise zero operands), so dk_b * dq_b * scale * log2 e * 2^s_b to about 22 bits. The scores are the fp32 sum over
+// the blocks of these products, started at -mref: ggml's per-block vec_dot arithmetic, with the softmax scale and the
+// base-2 conversion inside each block's factor instead of the dot of two fp16-rounded operands.
 // SKIP: a wave whose 32 rows are all past the call's rows only stages (its share of every tile's loads, dequant and LDS
 // stores, and the barriers). For calls with one row block narrower than 32 * NW rows. Without SKIP there is no branch
 // there: one costs 13-20 % on full row blocks, as it separates the next tile's loads from the QK MFMAs, which the
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     mm_h8 Qf[8];
     uint32_t dqb[4] = {0u, 0u, 0u, 0u};
     mm_prep_q<FMT, PRE, EX>(a, h, row, rlive, h2, Qf, dqb);
-    // EX: the B operand of the scale products, dq_b(row n) at k = 0 (lanes h2 = 0), zero elsewhere
+    // EX: the B operand of the scale products, the (hi, lo) pair of row n at k = 0, 1 (lanes h2 = 0), zero elsewhere
     uint32_t dqw[4];
     #pragma unroll
     for (int b = 0; b < 4; b++) dqw[b] = h2 == 0 ? dqb[b] : 0u;
@@ -226,7 +236,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     for (int db = 0; db < 4; db++) O[db] = (mm_f16){};
     float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
     const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit (!PRE)
-    const float cl2 = a.scale * MM_LOG2E;                             // EX: block-dot sum -> base-2 logit
     mm_f16 Cm = (mm_f16){};                                          // PRE: -mc in every element, the QK start value
     float mc = 0.0f;                                                 // PRE: mref once it is finite (0 before)
     const mm_h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
@@ -259,8 +268,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             va[db][mi] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
         };
         if constexpr (EX) {
-            // per block: the exact integer dot (two MFMAs), the exact scale products (one MFMA), their fp32 product
-            // summed over the blocks in block order
+            // per block: the integer dot times 2^-s_b (two MFMAs, exact), the products dk_b(key) * (hi + lo) (one MFMA:
+            // dk_b at k = 0 and 1, so dk_b * dq_b * scale * log2 e * 2^s_b to about 22 bits), their fp32 product summed
+            // over the blocks in block order from -mref: the base-2 logit minus the reference max
             const pa_u2 dk2 = *(const pa_u2 *) (Kt + MM_KT + MM_VT + 8 * n);   // key n's four fp16 block scales
             const uint32_t hmask = h2 == 0 ? 0xffffffffu : 0u;
             #pragma unroll
@@ -273,16 +283,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
                 }
                 mm_f16 Sb = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[2 * b], Qf[2 * b], (mm_f16){}, 0, 0, 0);
                 Sb = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[2 * b + 1], Qf[2 * b + 1], Sb, 0, 0, 0);
-                const uint32_t dkw = ((b & 1) ? dk2[b >> 1] >> 16 : dk2[b >> 1] & 0xffffu) & hmask;
+                const uint32_t dkw = pa_perm(0u, dk2[b >> 1], (b & 1) ? 0x03020302u : 0x01000100u) & hmask;
                 const mm_f16 Pb = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mm_h8, (pa_u4){dkw, 0u, 0u, 0u}),
                                                                          __builtin_bit_cast(mm_h8, (pa_u4){dqw[b], 0u, 0u, 0u}),
                                                                          (mm_f16){}, 0, 0, 0);
                 #pragma unroll
-                for (int v = 0; v < 16; v++) S[v] = b == 0 ? Pb[v] * Sb[v] : fmaf(Pb[v], Sb[v], S[v]);
+                for (int v = 0; v < 16; v++) S[v] = fmaf(Pb[v], Sb[v], b == 0 ? -mc : S[v]);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            #pragma unroll
-            for (int v = 0; v < 16; v++) S[v] = fmaf(S[v], cl2, -mc);  // base-2 logit minus the reference max
             #pragma unroll
             for (int kk = 0; kk < 8; kk++) v_read(kk);               // V^T after the block dots (registers), under the
                                                                      // softmax
