@@ -49,6 +49,40 @@ def test_sme_attn_partial_per_head(fmt):
     assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
 
 
+def test_sme_attn_partial_concurrent_threads():
+    """The reference server's sme_page (phone-attn.h:509-520) calls sme_attn_partial from one thread per KV head at
+    once, each thread with its own workspace (sme_ws_new): every call made concurrently returns, bit for bit, what
+    the same call returns alone, and that matches the fp64 oracle. ctypes releases the GIL for the foreign call, so
+    the eight calls overlap in the library (each workspace has its own stream and buffers)."""
+    import threading
+    nkv, nk = 8, 4096
+    K, V, Q, rs, hb = ref_case(bb.FMT_Q8_0, nkv, nk, 31)
+    ws = [bb.sme_ws_new() for _ in range(nkv)]
+
+    def call(h, O, m, l):
+        bb.sme_attn_partial(ws[h], Q[h * NR:], HD, K, V, rs, 1, nk, 1.0 / 16, 512, O[h * NR:], m[h * NR:], l[h * NR:],
+                            k_off=h * hb)
+
+    def outs():
+        return np.zeros((nkv * NR, HD), np.float32), np.zeros(nkv * NR, np.float32), np.zeros(nkv * NR, np.float32)
+
+    Oa, ma, la = outs()
+    for h in range(nkv):
+        call(h, Oa, ma, la)
+    for rep in range(4):
+        Ob, mb, lb = outs()
+        threads = [threading.Thread(target=call, args=(h, Ob, mb, lb)) for h in range(nkv)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert np.array_equal(Ob, Oa) and np.array_equal(mb, ma) and np.array_equal(lb, la), f"round {rep}"
+    ref = orc.attn_exact(orc.make_shape(nkv, NR, HD, orc.Q8_0, orc.QMODE_F16, scale=1.0 / 16, rs=rs), Q, K, V, nk)
+    eo, em, el = orc.rel_err(Oa, ma, la, *ref)
+    print(f"sme_attn_partial from {nkv} threads: max rel err O {eo:.3e} m {em:.3e} l {el:.3e}", flush=True)
+    assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
+
+
 def test_sme_attn_pipe_all_heads_and_empty():
     nkv, nk = 4, 4160
     K, V, Q, rs, hb = ref_case(bb.FMT_Q8_0, nkv, nk, 21)
