@@ -14,7 +14,9 @@
 // Q' is the query as fp16: PA_QMODE_GGML converts Q to K's vec_dot type as ggml's CPU flash_attn_ext does - q8_0 per
 // 32-block for quantized K (quantize_row_q8_0_ref), taken as fp16(d*q*scale*log2 e) so the scores come out in base-2
 // units, and fp16(q) for f16 K (the scale then multiplies the score); PA_QMODE_F16 takes fp16(q*scale) (the reference
-// engines' Qs, phone-attn.h:595-599). Online softmax in base 2 with a reference max that moves only when a score
+// engines' Qs, phone-attn.h:595-599). Calls of up to 128 rows per KV head (4-wave workgroups) over quantized K in the
+// ggml rounding take exact block dots instead (EX below): K staged as its integer quants, three MFMAs per 32-dim
+// block, ggml's per-block scaling in fp32. Online softmax in base 2 with a reference max that moves only when a score
 // exceeds it by more than 2^MM_PMAX (O is rescaled rarely); the exact max is tracked beside it and applied at the end.
 // The row sum adds the fp16 probabilities the PV MFMAs consume. Output: one split-K slot per workgroup (O unnormalised against the
 // base-2 max, max, sum), folded by merge_kernel, or the final (O, m, l) when the call has a single chunk.
