@@ -1,8 +1,9 @@
 """GPU: seeded random geometries through pa_hip_attn against the oracle, to catch dispatch and split-K geometry
-mistakes that the fixed shapes miss. Each case draws KV heads (odd counts included, so the decode kernel's head pairs
-give way to the matrix-core kernel), rows per KV head (1-300, across the decode, verify and prefill row blocks), head
-dim, format, query rounding, row padding, ragged pages (empty pages, single keys, more than one launch's worth of
-pages) and, for some, a forced split-K geometry (ws.set_split). Sizes keep the oracle within about a second per case.
+mistakes that the fixed shapes miss. Each case draws KV heads (1-32: odd counts, where the decode kernel's head pairs
+give way to the matrix-core kernel, and up to 16 head pairs), rows per KV head (1-300, across the decode, verify and
+prefill row blocks), head dim, format, query rounding, row padding, ragged pages (empty pages, single keys, more than
+one launch's worth of pages) and, for some, a forced split-K geometry (ws.set_split). Sizes keep the oracle within
+about a second per case.
 
 Tolerance 2e-3 as everywhere, on inputs inside the regimes the fixed tests pin at that bar: x8 outlier channels only
 where the scores are exact block dots (q8_0 / q4_0 in ggml rounding, up to 128 rows per KV head at head dim 128)."""
@@ -22,11 +23,11 @@ def draw(i: int):
     fmt = int(r.choice([bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16]))
     hd = int(r.choice([128, 256]))
     qmode = int(r.choice([bb.QMODE_GGML, bb.QMODE_F16]))
-    nkv = int(r.choice([1, 2, 3, 4, 5, 8, 9]))
+    nkv = int(r.choice([1, 2, 3, 4, 5, 8, 9, 16, 32]))
     rows = int(r.choice([1, 3, 6, 8, 9, 16, 33, 48, 100, 128, 129, 200, 300]))
     if i % 6 == 0:                                                   # the decode kernel's shape (even heads, <= 8 rows)
         fmt, hd, qmode = int(r.choice([bb.FMT_Q8_0, bb.FMT_Q4_0])), 128, bb.QMODE_GGML
-        nkv, rows = int(r.choice([2, 4, 8])), int(r.choice([1, 2, 5, 8]))
+        nkv, rows = int(r.choice([2, 4, 8, 16, 32])), int(r.choice([1, 2, 5, 8]))
     kind = r.integers(0, 10)
     if kind == 0:                                                    # more pages than one launch holds
         pages = [int(x) for x in r.integers(0, 40, size=int(r.integers(65, 80)))]
@@ -80,4 +81,5 @@ def test_draws_cover_the_kernels():
     assert any(c["hd"] == 256 and c["qmode"] == bb.QMODE_F16 for c in cs)
     assert any(c["hd"] == 256 and c["qmode"] == bb.QMODE_GGML and c["fmt"] != bb.FMT_F16 for c in cs)
     assert any(len(c["pages"]) > 64 for c in cs)
+    assert any(c["nkv"] >= 16 for c in dec) and any(c["nkv"] >= 16 and c not in dec for c in cs)
     assert any(c["split"] for c in cs) and any(c["outliers"] for c in cs)
