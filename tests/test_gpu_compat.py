@@ -35,7 +35,7 @@ def ref_case(fmt, nkv, nk, seed):
     return K, V, Q, rs, hb
 
 
-@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_F16])
+@pytest.mark.parametrize("fmt", [bb.FMT_Q8_0, bb.FMT_Q4_0, bb.FMT_F16])
 def test_sme_attn_partial_per_head(fmt):
     assert bb.sme2_available() == 1
     nkv, nk = 4, 4096
