@@ -75,6 +75,10 @@ def lib() -> C.CDLL:
     L.pa_hip_set_compat_shape.argtypes = [C.c_int, C.c_int]
     L.pa_hip_ws_free.restype = None
     L.pa_hip_ws_free.argtypes = [vp]
+    L.pa_hip_stream_wait.restype = C.c_int
+    L.pa_hip_stream_wait.argtypes = [vp, C.c_int]
+    L.pa_hip_shutdown.restype = C.c_int
+    L.pa_hip_shutdown.argtypes = [C.c_int]
     L.pa_hip_ws_new.restype = vp
     L.pa_hip_ws_new.argtypes = [C.c_int]
     L.pa_hip_ws_destroy.restype = None

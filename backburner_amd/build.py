@@ -4,6 +4,9 @@
 
 libpa_hip.so   the product: HIP kernels + the C ABI of include/phone_attn_hip.h
 libpa_synth.so bench/test support: synthetic HBM pages, device memory and event plumbing
+bin/pa-hip-serve  the reference's phone-attn server (phone-attn.h, compiled unchanged from the reference checkout named
+               by PA_REF_DIR, default /root/reference) with the HIP pa::engine of integration/; built only where that
+               checkout is present (the built binary travels with the tree)
 """
 from __future__ import annotations
 
@@ -18,6 +21,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = ROOT / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CLANGXX = "/opt/rocm/llvm/bin/clang++"
+REF = Path(os.environ.get("PA_REF_DIR", "/root/reference"))
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
@@ -69,8 +74,27 @@ def build(verbose: bool = False) -> None:
         tmp = PKG / (lib + ".tmp")
         _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", f"-Wl,-soname,{lib}", *objs, "-o", str(tmp)], verbose)
         os.replace(tmp, PKG / lib)
+    build_server(verbose)
     # the oracle (test infrastructure) and, where the reference checkout exists, its pa-tool builds
     _run(["make", "-s", "-C", str(ROOT / "oracle")], verbose)
+
+
+def build_server(verbose: bool = False) -> None:
+    """bin/pa-hip-serve: integration/pa_hip_serve.cpp (pa::server of phone-attn.h, unchanged, around the HIP engine)
+    linked against libpa_hip.so. phone-attn.h compiles on Linux with clang++ given two macro definitions:
+    TARGET_OS_IPHONE=0 (Apple's TargetConditionals value off the iPhone; phone-attn.h:413 uses it as an expression) and an
+    empty __builtin_arm_yield() (an Arm spin hint, phone-attn.h:371). Nothing else is substituted."""
+    hdr = REF / "phone-attn" / "phone-attn.h"
+    if not hdr.exists():
+        return
+    out = PKG / "bin" / "pa-hip-serve"
+    out.parent.mkdir(exist_ok=True)
+    integ = PKG / "integration"
+    _run([CLANGXX, "-std=c++17", "-O2", "-DTARGET_OS_IPHONE=0", "-D__builtin_arm_yield()=((void)0)", "-Wno-unused-result",
+          "-pthread", "-D__HIP_PLATFORM_AMD__", f"-I{hdr.parent}", f"-I{ROOT / 'include'}", f"-I{integ}",
+          "-I/opt/rocm/include", "-o", str(out) + ".tmp", str(integ / "pa_hip_serve.cpp"), f"-L{PKG}", "-lpa_hip",
+          "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,/opt/rocm/lib"], verbose)
+    os.replace(str(out) + ".tmp", out)
 
 
 if __name__ == "__main__":

@@ -7,12 +7,14 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/phone_attn_hip.h"
@@ -74,12 +76,16 @@ struct pa_hip_ws {
     std::vector<void *> retired;
     // split-K geometry overrides (pa_hip_ws_set_split); 0 = the default geometry
     int dec_groups = 0, mma_workgroups = 0;
-    // the sme_* compatibility path: its own stream and staging buffers
+    // the sme_* compatibility path: its own stream, device staging and a pinned host staging area (host rows are copied
+    // into it on the calling thread, so every transfer is pinned <-> device); `broken` after a call whose wait timed
+    // out (its transfers may still land in the staging areas, so the workspace is not used again)
     hipStream_t stream = nullptr;
     uint8_t * dk = nullptr; size_t dk_cap = 0;
     uint8_t * dv = nullptr; size_t dv_cap = 0;
     float * dq = nullptr; size_t dq_cap = 0;
     float * dout = nullptr; size_t dout_cap = 0;
+    char * hst = nullptr; size_t hst_cap = 0;
+    bool broken = false;
     // measurement hook (pa_hip_ws_time_next)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     // pa_hip_attn_reply: (O, m, l) staging
@@ -132,11 +138,13 @@ extern "C" pa_hip_ws * pa_hip_ws_new(int device) {
 
 extern "C" void pa_hip_ws_destroy(pa_hip_ws * w) {
     if (!w) return;
+    if (w->broken) return;   // a timed-out call may still be using its buffers: they are left to the process
     (void) hipDeviceSynchronize();
     for (void * p : {(void *) w->po, (void *) w->pml, (void *) w->apart, (void *) w->acount, (void *) w->dk,
                      (void *) w->dv, (void *) w->dq, (void *) w->dout, (void *) w->ro, (void *) w->rml})
         (void) hipFree(p);
     for (void * p : w->retired) (void) hipFree(p);
+    if (w->hst) (void) hipHostFree(w->hst);
     if (w->stream) (void) hipStreamDestroy(w->stream);
     delete w;
 }
@@ -736,13 +744,49 @@ void fail_out(float * O, float * m, float * l, size_t rows, int hd) {
     for (size_t r = 0; r < rows; r++) { if (m) m[r] = -INFINITY; if (l) l[r] = 0.0f; }
 }
 
-// one synchronous call of the engine path for `nkv` heads at K/V (host or device), reference rounding (f16 Q*scale)
+// sme_* calls in flight, and the gate pa_hip_shutdown closes (new calls then fail at once)
+std::atomic<int> g_compat_inflight{0};
+std::atomic<bool> g_compat_closed{false};
+struct InFlight {
+    InFlight() { g_compat_inflight.fetch_add(1); }
+    ~InFlight() { g_compat_inflight.fetch_sub(1); }
+};
+
+// wait limit of the synchronous calls (PA_HIP_WAIT_MS, default 30 s): far above any call's run time, so that a stalled
+// device or runtime ends the call with an error instead of blocking its thread for good
+int wait_limit_ms() {
+    static const int v = [] { const int x = env_int("PA_HIP_WAIT_MS", 30000); return x > 0 ? x : 30000; }();
+    return v;
+}
+
+// pinned host staging of the workspace with room for `need` bytes (its stream is idle between sme_* calls)
+bool ensure_pinned(pa_hip_ws * w, size_t need) {
+    if (need <= w->hst_cap && w->hst) return true;
+    if (w->hst) { (void) hipHostFree(w->hst); w->hst = nullptr; w->hst_cap = 0; }
+    const size_t sz = std::max<size_t>({need, 2 * w->hst_cap, 1u << 16});
+    void * p = nullptr;
+    if (!hip_ok(hipHostMalloc(&p, sz, hipHostMallocDefault), "hipHostMalloc sme_* staging")) return false;
+    w->hst = (char *) p; w->hst_cap = sz;
+    return true;
+}
+
+size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+
+// one synchronous call of the engine path for `nkv` heads at K/V (host or device), reference rounding (f16 Q*scale).
+// Host buffers are never handed to the HIP runtime: K/V spans and Q rows are copied into the workspace's pinned staging
+// on the calling thread, only pinned <-> device copies are enqueued, and the results come back through the same
+// staging. So concurrent calls from several threads (the server's sme_page, phone-attn.h:509-520) never make the
+// runtime pin or stage the callers' pageable pages, and a call's host buffers are not touched by a transfer after it
+// returns. The wait for the stream is bounded (wait_limit_ms).
 bool compat_call(pa_hip_ws * w, const float * Q, int qrs, int qhs, const uint8_t * K, const uint8_t * V, size_t rs, size_t hb,
                  int fmt, int nkv, int nk, float scale, float * O, float * m, float * l) {
+    InFlight inflight;
     int NR, HD;
     compat_shape(NR, HD);
     const size_t rows = (size_t) nkv * NR;
+    if (g_compat_closed.load()) { set_err("sme_*: the library is shut down (pa_hip_shutdown)"); return false; }
     if (!w) { set_err("sme_*: null workspace"); return false; }
+    if (w->broken) { set_err("sme_*: workspace unusable after a call that timed out"); return false; }
     if (fmt < 0 || fmt > 2) { set_err("sme_*: is_q8 must be 0, 1 or 2"); return false; }
     if (nk < 0) { set_err("sme_*: nk < 0"); return false; }
     if (nk == 0) {   // sme_attn.c:281-282: m starts at -1e30, l and O at 0
@@ -755,27 +799,33 @@ bool compat_call(pa_hip_ws * w, const float * Q, int qrs, int qhs, const uint8_t
     const uint32_t hbmin = head_bytes(fmt, HD);
     // K/V: device pointers are used in place; host rows are staged (rows [0, nk) of every head in the span)
     const size_t span = (size_t) (nk - 1) * rs + (size_t) (nkv - 1) * hb + hbmin;
+    const bool k_host = !is_device_ptr(K), v_host = !is_device_ptr(V);
+    const size_t q_b = rows * HD * sizeof(float), o_b = rows * (HD + 2) * sizeof(float);
+    // pinned layout: [K span][V span][Q][O, m, l]
+    const size_t hk_off = 0, hv_off = k_host ? al256(span) : 0, hq_off = hv_off + (v_host ? al256(span) : 0);
+    const size_t ho_off = hq_off + al256(q_b);
+    if (!ensure_pinned(w, ho_off + o_b)) return false;
     const uint8_t * dK = K, * dV = V;
-    if (!is_device_ptr(K)) {
-        if (!ensure(w, w->dk, w->dk_cap, span, st, false, "hipMalloc K staging") ||
-            !hip_ok(hipMemcpyAsync(w->dk, K, span, hipMemcpyHostToDevice, st), "K upload"))
-            return false;
+    if (k_host) {
+        if (!ensure(w, w->dk, w->dk_cap, span, st, false, "hipMalloc K staging")) return false;
+        std::memcpy(w->hst + hk_off, K, span);
+        if (!hip_ok(hipMemcpyAsync(w->dk, w->hst + hk_off, span, hipMemcpyHostToDevice, st), "K upload")) return false;
         dK = w->dk;
     }
-    if (!is_device_ptr(V)) {
-        if (!ensure(w, w->dv, w->dv_cap, span, st, false, "hipMalloc V staging") ||
-            !hip_ok(hipMemcpyAsync(w->dv, V, span, hipMemcpyHostToDevice, st), "V upload"))
-            return false;
+    if (v_host) {
+        if (!ensure(w, w->dv, w->dv_cap, span, st, false, "hipMalloc V staging")) return false;
+        std::memcpy(w->hst + hv_off, V, span);
+        if (!hip_ok(hipMemcpyAsync(w->dv, w->hst + hv_off, span, hipMemcpyHostToDevice, st), "V upload")) return false;
         dV = w->dv;
     }
-    const size_t q_b = rows * HD * sizeof(float), o_b = rows * (HD + 2) * sizeof(float);
     if (!ensure(w, w->dq, w->dq_cap, q_b, st, false, "hipMalloc Q staging") ||
         !ensure(w, w->dout, w->dout_cap, o_b, st, false, "hipMalloc O staging"))
         return false;
+    float * hq = (float *) (w->hst + hq_off);
     for (int h = 0; h < nkv; h++)
-        if (!hip_ok(hipMemcpy2DAsync(w->dq + (size_t) h * NR * HD, HD * sizeof(float), Q + (size_t) h * qhs, (size_t) qrs * sizeof(float),
-                                     HD * sizeof(float), NR, hipMemcpyHostToDevice, st), "Q upload"))
-            return false;
+        for (int r = 0; r < NR; r++)
+            std::memcpy(hq + ((size_t) h * NR + r) * HD, Q + (size_t) h * qhs + (size_t) r * qrs, HD * sizeof(float));
+    if (!hip_ok(hipMemcpyAsync(w->dq, hq, q_b, hipMemcpyHostToDevice, st), "Q upload")) return false;
     pa_hip_shape s;
     s.nkv = (uint32_t) nkv; s.rows = (uint32_t) NR; s.hd = (uint32_t) HD; s.fmt = (uint32_t) fmt;
     s.rs = (uint32_t) rs; s.hb = (uint32_t) hb; s.qmode = PA_QMODE_F16; s.scale = scale;
@@ -784,11 +834,15 @@ bool compat_call(pa_hip_ws * w, const float * Q, int qrs, int qhs, const uint8_t
     const uint32_t nkeys[1] = {(uint32_t) nk};
     float * dO = w->dout, * dm = dO + rows * HD, * dl = dm + rows;
     if (pa_hip_attn(w, &s, kp, vp, nkeys, 1, w->dq, dO, dm, dl, st) != 0) return false;
-    if (!hip_ok(hipMemcpyAsync(O, dO, rows * HD * sizeof(float), hipMemcpyDeviceToHost, st), "O download") ||
-        !hip_ok(hipMemcpyAsync(m, dm, rows * sizeof(float), hipMemcpyDeviceToHost, st), "m download") ||
-        !hip_ok(hipMemcpyAsync(l, dl, rows * sizeof(float), hipMemcpyDeviceToHost, st), "l download") ||
-        !hip_ok(hipStreamSynchronize(st), "sme_* call"))
+    float * ho = (float *) (w->hst + ho_off);
+    if (!hip_ok(hipMemcpyAsync(ho, dO, o_b, hipMemcpyDeviceToHost, st), "O, m, l download")) return false;
+    if (pa_hip_stream_wait(st, wait_limit_ms()) != 0) {
+        if (hipStreamQuery(st) == hipErrorNotReady) w->broken = true;
         return false;
+    }
+    std::memcpy(O, ho, rows * HD * sizeof(float));
+    std::memcpy(m, ho + rows * HD, rows * sizeof(float));
+    std::memcpy(l, ho + rows * (HD + 1), rows * sizeof(float));
     return true;
 }
 
@@ -810,6 +864,39 @@ extern "C" void * sme_ws_new(void) {
 extern "C" void * sme_pipe_new(int nh) { (void) nh; return sme_ws_new(); }
 
 extern "C" void pa_hip_ws_free(void * w) { pa_hip_ws_destroy((pa_hip_ws *) w); }
+
+extern "C" int pa_hip_stream_wait(void * stream, int timeout_ms) {
+    hipStream_t st = (hipStream_t) stream;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (unsigned spin = 0;; spin++) {
+        const hipError_t e = hipStreamQuery(st);
+        if (e == hipSuccess) return 0;
+        if (e != hipErrorNotReady) { hip_ok(e, "pa_hip_stream_wait"); return -1; }
+        (void) hipGetLastError();   // not-ready is a state, not an error of this thread
+        const auto ms = std::chrono::duration_cast<std::chrono::milliseconds>(std::chrono::steady_clock::now() - t0).count();
+        if (timeout_ms >= 0 && ms >= timeout_ms) {
+            set_err("pa_hip_stream_wait: the stream's work did not finish within " + std::to_string(timeout_ms) + " ms");
+            return -1;
+        }
+        // short calls return within microseconds: spin a little, then poll every 50 us
+        if (spin < 1000) std::this_thread::yield();
+        else std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+}
+
+extern "C" int pa_hip_shutdown(int timeout_ms) {
+    g_compat_closed.store(true);
+    const auto t0 = std::chrono::steady_clock::now();
+    while (g_compat_inflight.load() > 0) {
+        const auto ms = std::chrono::duration_cast<std::chrono::milliseconds>(std::chrono::steady_clock::now() - t0).count();
+        if (timeout_ms >= 0 && ms >= timeout_ms) {
+            set_err("pa_hip_shutdown: " + std::to_string(g_compat_inflight.load()) + " sme_* calls still running");
+            return -1;
+        }
+        std::this_thread::sleep_for(std::chrono::microseconds(200));
+    }
+    return 0;
+}
 
 extern "C" int sme2_available(void) { return device_usable() ? 1 : 0; }
 

@@ -16,11 +16,16 @@
 // [ng][nkv*NR] rows ((0, -inf, 0) for the tokens the call did not have); one copy back. end() waits and copies
 // (O, m, l) out; it returns the attention's GPU ms.
 // Failure: begin() returns false (the server answers "GPU engine failed to start"); end() returns -1 with
-// O = 0, m = -inf, l = 0, the Metal engine's failure value (pa-metal.mm:932-937).
+// O = 0, m = -inf, l = 0, the Metal engine's failure value (pa-metal.mm:932-937). Every wait on the engine's stream is
+// bounded (pa_hip_stream_wait, PA_HIP_WAIT_MS, default 30 s): a stalled call fails instead of blocking the server.
+// close() (the process's exit path) refuses further calls and waits until the one in flight has ended.
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cmath>
+#include <condition_variable>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -44,7 +49,7 @@ struct hip_engine : pa::engine {
         return true;
     }
     ~hip_engine() override {
-        if (st_) (void) hipStreamSynchronize(st_);
+        if (st_ && !idle(wait_ms())) return;   // work still in flight after the limit: leave its buffers to the process
         if (ws_) pa_hip_ws_destroy(ws_);
         (void) hipFree(dbuf_);
         (void) hipHostFree(hbuf_);
@@ -67,7 +72,7 @@ struct hip_engine : pa::engine {
         return true;
     }
     void free_page(pa::page & p) override {
-        (void) hipStreamSynchronize(st_);                            // no copy of this page in flight
+        if (!idle(wait_ms())) { p = pa::page(); return; }            // a copy of this page may be in flight: leak it
         {
             std::lock_guard<std::mutex> lk(mu_);
             held_.erase(p.hk);
@@ -79,6 +84,41 @@ struct hip_engine : pa::engine {
 
     bool begin(const pa::page * pages, const uint32_t * nkeys, int n_pages, const uint16_t * Qs, const pa::config_req & cfg,
                int ng) override {
+        {
+            std::lock_guard<std::mutex> lk(gate_mu_);
+            if (closing_) return fail("the engine is closing");
+            in_call_ = true;   // until end(), or until this begin() fails
+        }
+        if (!start(pages, nkeys, n_pages, Qs, cfg, ng)) { leave(); return false; }
+        return true;
+    }
+
+    double end(float * O, float * m, float * l) override {
+        const double r = finish(O, m, l);
+        leave();
+        return r;
+    }
+
+    // the process's exit path: refuse new calls, wait (up to timeout_ms) until the call in flight has ended and the
+    // stream is idle. Returns true when idle.
+    bool close(int timeout_ms) {
+        std::unique_lock<std::mutex> lk(gate_mu_);
+        closing_ = true;
+        if (!gate_cv_.wait_for(lk, std::chrono::milliseconds(timeout_ms), [this] { return !in_call_; })) return false;
+        lk.unlock();
+        return !st_ || idle(timeout_ms);
+    }
+
+    double exec_ms() const override { return last_ms_; }
+    std::string describe() override {
+        return "hip MI355X (libpa_hip) rows_uploaded=" + std::to_string(rows_up_) + (tracked_ ? " tracked=1" : " tracked=0") +
+               " call_rows_per_kv_head=" + std::to_string(last_rows_);
+    }
+    uint64_t rows_uploaded() const { return rows_up_; }   // K/V rows copied to HBM since init
+
+private:
+    bool start(const pa::page * pages, const uint32_t * nkeys, int n_pages, const uint16_t * Qs, const pa::config_req & cfg,
+               int ng) {
         nkv_ = (uint32_t) cfg.n_head_kv; ng_ = (uint32_t) ng;
         nt_ = (ng == 1 && ntok_hint >= 1 && ntok_hint < 8) ? (uint32_t) ntok_hint : 0;
         const uint32_t rows = nt_ ? (pa::NR / 8) * nt_ : ng_ * pa::NR;          // call rows per KV head
@@ -111,10 +151,9 @@ struct hip_engine : pa::engine {
         return true;
     }
 
-    double end(float * O, float * m, float * l) override {
+    double finish(float * O, float * m, float * l) {
         const size_t srows = (size_t) ng_ * nkv_ * pa::NR, qn = srows * pa::HD;
-        if (hipStreamSynchronize(st_) != hipSuccess) {
-            fail("hipStreamSynchronize");
+        if (!idle(wait_ms())) {
             for (size_t i = 0; i < qn; i++) O[i] = 0.0f;
             for (size_t i = 0; i < srows; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
             return -1.0;
@@ -127,15 +166,23 @@ struct hip_engine : pa::engine {
         last_ms_ = ms;
         return ms;
     }
-
-    double exec_ms() const override { return last_ms_; }
-    std::string describe() override {
-        return "hip MI355X (libpa_hip) rows_uploaded=" + std::to_string(rows_up_) + (tracked_ ? " tracked=1" : " tracked=0") +
-               " call_rows_per_kv_head=" + std::to_string(last_rows_);
+    void leave() {
+        {
+            std::lock_guard<std::mutex> lk(gate_mu_);
+            in_call_ = false;
+        }
+        gate_cv_.notify_all();
     }
-    uint64_t rows_uploaded() const { return rows_up_; }   // K/V rows copied to HBM since init
+    static int wait_ms() {
+        static const int v = [] { const char * e = getenv("PA_HIP_WAIT_MS"); const int x = e ? atoi(e) : 0; return x > 0 ? x : 30000; }();
+        return v;
+    }
+    // the engine's stream has finished its work (bounded wait); false on a stream error or after the limit
+    bool idle(int timeout_ms) {
+        if (pa_hip_stream_wait(st_, timeout_ms) == 0) return true;
+        return fail(std::string("engine stream: ") + pa_hip_last_error());
+    }
 
-private:
     // the page engine the server reports TRUNCATE / CONFIG to; it takes no keys (ready() = 0), builds nothing
     struct tracker : pa::page_engine {
         hip_engine * e = nullptr;
@@ -183,7 +230,7 @@ private:
     static size_t al(size_t b) { return (b + 255) / 256 * 256; }
     bool ensure(size_t dev_b, size_t host_b) {
         if (dev_b <= dcap_ && host_b <= hcap_) return true;
-        (void) hipStreamSynchronize(st_);
+        if (!idle(wait_ms())) return false;
         (void) hipFree(dbuf_); (void) hipHostFree(hbuf_);
         dbuf_ = nullptr; hbuf_ = nullptr; dcap_ = hcap_ = 0;
         if (hipMalloc((void **) &dbuf_, dev_b) != hipSuccess) return fail("hipMalloc call buffers");
@@ -204,6 +251,9 @@ private:
     tracker tracker_;
     std::mutex mu_;
     std::unordered_map<void *, held> held_;   // per page (keyed by its HBM K copy)
+    std::mutex gate_mu_;                      // close(): no call in flight, none started after it
+    std::condition_variable gate_cv_;
+    bool closing_ = false, in_call_ = false;
     bool tracked_ = false;
     uint64_t rows_up_ = 0;
 };

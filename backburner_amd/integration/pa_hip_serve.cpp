@@ -7,8 +7,11 @@
 //   pa-hip-serve [port] [threads]
 //
 // SIGTERM / SIGINT end the process with a normal exit (exit handlers run, so a profiler wrapping the server writes its
-// results); send it between sessions. Built by oracle/Makefile where the reference checkout (phone-attn.h) is present;
-// the server's non-GPU pages go to the sme_* C ABI, which libpa_hip.so also exports.
+// results). Before it exits, the engine refuses new calls and the one in flight (if any) runs to its end, and the sme_*
+// calls of the server's CPU-engine pages (libpa_hip.so also exports that C ABI) are closed the same way, each wait
+// bounded (PA_HIP_WAIT_MS): no HIP call is still running when the exit handlers tear the runtime down. A session in
+// progress then gets error replies. Built by backburner_amd/build.py where the reference checkout (phone-attn.h) is
+// present.
 #include "phone-attn.h"
 #include "pa_hip_engine.h"
 
@@ -41,5 +44,11 @@ int main(int argc, char ** argv) {
         g_stop.store(2);
     }).detach();
     while (g_stop.load() == 0) std::this_thread::sleep_for(std::chrono::milliseconds(20));
-    std::exit(g_stop.load() == 2 ? 1 : 0);   // the serving thread stays blocked in accept()
+    const char * e = getenv("PA_HIP_WAIT_MS");
+    const int limit = e && atoi(e) > 0 ? atoi(e) : 30000;
+    const bool eng_idle = eng.close(limit);
+    const bool sme_idle = pa_hip_shutdown(limit) == 0;
+    if (!eng_idle || !sme_idle)
+        fprintf(stderr, "pa-hip-serve: exiting with GPU work still running (%s)\n", eng_idle ? pa_hip_last_error() : eng.error.c_str());
+    std::exit(g_stop.load() == 2 ? 1 : 0);   // the serving thread stays blocked in accept() or in its session
 }

@@ -67,6 +67,18 @@ int pa_hip_set_compat_shape(int nr, int hd);
 /* Release a handle from sme_ws_new / sme_pipe_new (the reference never frees them). */
 void pa_hip_ws_free(void * w);
 
+/* No counterpart in the reference (its engines wait without a limit, pa-metal.mm:928-931): wait until the work enqueued
+ * on `stream` (a hipStream_t) has finished, for at most timeout_ms (< 0: no limit). Returns 0 when done, -1 on a stream
+ * error or when the limit passed first (pa_hip_last_error() says which). The sme_* calls wait through this with the
+ * limit PA_HIP_WAIT_MS (environment, default 30000); a call that runs out of time fails like any other (m = -inf,
+ * l = 0, O = 0) and its workspace refuses further calls. */
+int pa_hip_stream_wait(void * stream, int timeout_ms);
+
+/* No counterpart in the reference: for a process about to exit (the server's signal handler). New sme_* calls fail from
+ * now on; waits up to timeout_ms (< 0: no limit) for the ones running to return. Returns 0 when none is left, -1
+ * otherwise. */
+int pa_hip_shutdown(int timeout_ms);
+
 /* ---------------------------------------------------------------- 2. device-resident engine path */
 
 enum { PA_FMT_F16 = 0, PA_FMT_Q8_0 = 1, PA_FMT_Q4_0 = 2 };   /* config_req.is_q8 (phone-attn.h:15, 88) */

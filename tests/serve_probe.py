@@ -2,7 +2,7 @@
 prints one JSON line: the client's wall time per ATTN, the engine's GPU time per call, and how many K/V rows the engine
 uploaded to HBM - once when the first call reads the held pages, then only rows appended since.
 
-    python3 backburner_amd/integration/serve_probe.py [--keys 131072] [--calls 20] [--ntok 1] [--server PATH]
+    python3 tests/serve_probe.py [--keys 131072] [--calls 20] [--ntok 1] [--server PATH]
 
 Layout: the reference's shape (4 KV heads, 48 query rows, head dim 256), q8_0 rows of random quants, one layer. The
 probe starts the server on a free loopback port, sends CONFIG, APPENDs the keys in messages of 4,096 rows, makes three
@@ -22,7 +22,7 @@ from pathlib import Path
 
 import numpy as np
 
-ROOT = Path(__file__).resolve().parents[2]
+ROOT = Path(__file__).resolve().parents[1]
 sys.path.insert(0, str(ROOT))
 from backburner_amd.patn_wire import HD, NR, Client  # noqa: E402
 
@@ -48,7 +48,7 @@ def free_port() -> int:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--server", default=str(ROOT / "oracle" / "_ref" / "pa-hip-serve"))
+    ap.add_argument("--server", default=str(ROOT / "backburner_amd" / "bin" / "pa-hip-serve"))
     ap.add_argument("--keys", type=int, default=131072)
     ap.add_argument("--calls", type=int, default=20)
     ap.add_argument("--ntok", type=int, default=1)

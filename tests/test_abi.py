@@ -96,3 +96,20 @@ def test_no_gpu_fails_loudly():
         pytest.skip("a GPU is present: the no-GPU path is not observable here")
     n, w, s, *msg = out.stdout.split(maxsplit=3)
     assert n == "0" and w == "None" and s == "None" and msg and ("device" in msg[0])
+
+
+def test_shutdown_gate_refuses_new_calls():
+    """pa_hip_shutdown (the server's exit path): with no sme_* call running it returns 0 at once, and every sme_* call
+    after it fails with that reason (run in a child process: the gate is process-wide)."""
+    code = (
+        "import ctypes as C\n"
+        f"L = C.CDLL({str(LIB)!r})\n"
+        "L.pa_hip_last_error.restype = C.c_char_p\n"
+        "rc = L.pa_hip_shutdown(1000)\n"
+        "f = (C.c_float * (48 * 256))()\n"
+        "L.sme_attn_partial(None, f, 256, None, None, C.c_size_t(1088), 1, 64, C.c_float(0.0625), 512, f, f, f)\n"
+        "print(rc, L.pa_hip_last_error().decode())\n")
+    out = subprocess.run(["python3", "-c", code], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    rc, msg = out.stdout.split(maxsplit=1)
+    assert rc == "0" and "shut down" in msg, out.stdout

@@ -1,7 +1,7 @@
 """GPU: the reference's C ABI exported by libpa_hip.so (sme_attn_partial / sme_attn_pipe, phone-attn.h:63-71) with host
 buffers at the reference shape (48 rows per KV head, head dim 256); the reference's own pa-tool, compiled unchanged
 and linked against libpa_hip.so, running its loopback fp64 check on the GPU engine; and the reference's unchanged
-pa::server with the product's HIP pa::engine (oracle/_ref/pa-hip-serve), driven over the PATN wire by the unchanged
+pa::server with the product's HIP pa::engine (backburner_amd/bin/pa-hip-serve), driven over the PATN wire by the unchanged
 pa-tool client with every page on the GPU."""
 import re
 from pathlib import Path
@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 ROOT = Path(__file__).resolve().parents[1]
 TOOL_HIP = ROOT / "oracle" / "_ref" / "pa-tool-hip"
 TOOL_CPU = ROOT / "oracle" / "_ref" / "pa-tool-cpu"
-SERVE_HIP = ROOT / "oracle" / "_ref" / "pa-hip-serve"
+SERVE_HIP = ROOT / "backburner_amd" / "bin" / "pa-hip-serve"
 NR, HD = 48, 256
 
 
@@ -53,34 +53,70 @@ def test_sme_attn_partial_concurrent_threads():
     """The reference server's sme_page (phone-attn.h:509-520) calls sme_attn_partial from one thread per KV head at
     once, each thread with its own workspace (sme_ws_new): every call made concurrently returns, bit for bit, what
     the same call returns alone, and that matches the fp64 oracle. ctypes releases the GIL for the foreign call, so
-    the eight calls overlap in the library (each workspace has its own stream and buffers)."""
+    the eight calls overlap in the library (each workspace has its own stream, device buffers and pinned staging; the
+    threads' K/V spans overlap in host memory, as the server's heads of one page do)."""
     import threading
     nkv, nk = 8, 4096
     K, V, Q, rs, hb = ref_case(bb.FMT_Q8_0, nkv, nk, 31)
     ws = [bb.sme_ws_new() for _ in range(nkv)]
+    try:
+        def call(h, O, m, l):
+            bb.sme_attn_partial(ws[h], Q[h * NR:], HD, K, V, rs, 1, nk, 1.0 / 16, 512, O[h * NR:], m[h * NR:], l[h * NR:],
+                                k_off=h * hb)
 
-    def call(h, O, m, l):
-        bb.sme_attn_partial(ws[h], Q[h * NR:], HD, K, V, rs, 1, nk, 1.0 / 16, 512, O[h * NR:], m[h * NR:], l[h * NR:],
-                            k_off=h * hb)
+        def outs():
+            return np.zeros((nkv * NR, HD), np.float32), np.zeros(nkv * NR, np.float32), np.zeros(nkv * NR, np.float32)
 
-    def outs():
-        return np.zeros((nkv * NR, HD), np.float32), np.zeros(nkv * NR, np.float32), np.zeros(nkv * NR, np.float32)
-
-    Oa, ma, la = outs()
-    for h in range(nkv):
-        call(h, Oa, ma, la)
-    for rep in range(4):
-        Ob, mb, lb = outs()
-        threads = [threading.Thread(target=call, args=(h, Ob, mb, lb)) for h in range(nkv)]
-        for t in threads:
-            t.start()
-        for t in threads:
-            t.join()
-        assert np.array_equal(Ob, Oa) and np.array_equal(mb, ma) and np.array_equal(lb, la), f"round {rep}"
+        Oa, ma, la = outs()
+        for h in range(nkv):
+            call(h, Oa, ma, la)
+        for rep in range(4):
+            print(f"concurrent round {rep}", flush=True)
+            Ob, mb, lb = outs()
+            threads = [threading.Thread(target=call, args=(h, Ob, mb, lb)) for h in range(nkv)]
+            for t in threads:
+                t.start()
+            for t in threads:
+                t.join()
+            assert np.array_equal(Ob, Oa) and np.array_equal(mb, ma) and np.array_equal(lb, la), f"round {rep}"
+    finally:
+        for w in ws:
+            bb.lib().pa_hip_ws_free(w)
     ref = orc.attn_exact(orc.make_shape(nkv, NR, HD, orc.Q8_0, orc.QMODE_F16, scale=1.0 / 16, rs=rs), Q, K, V, nk)
     eo, em, el = orc.rel_err(Oa, ma, la, *ref)
     print(f"sme_attn_partial from {nkv} threads: max rel err O {eo:.3e} m {em:.3e} l {el:.3e}", flush=True)
     assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
+
+
+def test_stream_wait_is_bounded():
+    """pa_hip_stream_wait, the wait every synchronous call uses: with a 0 ms limit on a stream that still has several
+    milliseconds of attention work queued it returns -1 and says so; with a generous limit it returns 0 once the work
+    is done, and the results equal a call made alone."""
+    nkv, rows, hd, nk = 8, 4096, 128, 16384
+    K, V, Q, rs = (lambda hb: (orc.fill_rows(41, orc.Q8_0, nkv, hd, nk, rs=nkv * hb), orc.fill_rows(42, orc.Q8_0, nkv, hd, nk, rs=nkv * hb),
+                               orc.normal(43, 0, nkv * rows * hd).reshape(nkv * rows, hd), nkv * hb))(orc.head_bytes(orc.Q8_0, hd))
+    shape = bb.make_shape(nkv, rows, hd, bb.FMT_Q8_0, rs=rs)
+    ws = bb.Workspace()
+    pages = bb.pages_from_rows(K, V, rs)
+    dq = bb.DeviceBuffer.from_array(Q)
+    outs = [bb.DeviceBuffer(nkv * rows * hd * 4), bb.DeviceBuffer(nkv * rows * 4), bb.DeviceBuffer(nkv * rows * 4)]
+    try:
+        ws.attn(shape, pages, dq.ptr, *(b.ptr for b in outs))
+        bb.device_sync()
+        first = [b.download(np.float32) for b in outs]
+        for _ in range(20):                       # about 6 ms of queued work on the null stream
+            ws.attn(shape, pages, dq.ptr, *(b.ptr for b in outs))
+        rc0 = bb.lib().pa_hip_stream_wait(None, 0)
+        msg = bb.last_error()
+        rc1 = bb.lib().pa_hip_stream_wait(None, 60000)
+        print(f"wait(0 ms) -> {rc0} ({msg}); wait(60 s) -> {rc1}", flush=True)
+        assert rc0 == -1 and "did not finish" in msg
+        assert rc1 == 0
+        for a, b in zip(first, outs):
+            assert np.array_equal(a, b.download(np.float32))
+    finally:
+        bb.device_sync()
+        ws.close()
 
 
 def test_sme_attn_pipe_all_heads_and_empty():
@@ -130,7 +166,7 @@ def test_reference_patool_big_on_gpu_engine():
 
 
 needs_serve = pytest.mark.skipif(not (SERVE_HIP.exists() and TOOL_CPU.exists()),
-                                 reason="oracle/_ref/pa-hip-serve not built (reference checkout absent at build time)")
+                                 reason="backburner_amd/bin/pa-hip-serve not built (reference checkout absent at build time)")
 
 
 @needs_serve

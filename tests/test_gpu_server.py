@@ -1,4 +1,4 @@
-"""The reference's unchanged pa::server over the PATN wire, with the HIP engine (oracle/_ref/pa-hip-serve): pages stay in
+"""The reference's unchanged pa::server over the PATN wire, with the HIP engine (backburner_amd/bin/pa-hip-serve): pages stay in
 HBM between calls, only appended rows are uploaded, TRUNCATE to the middle of a page followed by APPEND of different
 rows to the same count is seen, and one-group calls with fewer than 8 tokens compute only the real rows.
 
@@ -25,7 +25,7 @@ from backburner_amd.patn_wire import HD, NR, Client
 from tests.test_ref_patool import free_port
 
 ROOT = Path(__file__).resolve().parents[1]
-SERVE_HIP = ROOT / "oracle" / "_ref" / "pa-hip-serve"
+SERVE_HIP = ROOT / "backburner_amd" / "bin" / "pa-hip-serve"
 TOOL_CPU = ROOT / "oracle" / "_ref" / "pa-tool-cpu"
 NKV, FMT = 4, orc.Q8_0
 HB = orc.head_bytes(FMT, HD)
@@ -168,7 +168,7 @@ def scenario(cmd: list, ntok: int, gpu: bool):
 
 
 needs_cpu_server = pytest.mark.skipif(not TOOL_CPU.exists(), reason="oracle/_ref/pa-tool-cpu not built (reference checkout absent at build time)")
-needs_hip_server = pytest.mark.skipif(not SERVE_HIP.exists(), reason="oracle/_ref/pa-hip-serve not built (reference checkout absent at build time)")
+needs_hip_server = pytest.mark.skipif(not SERVE_HIP.exists(), reason="backburner_amd/bin/pa-hip-serve not built (reference checkout absent at build time)")
 
 
 @needs_cpu_server
@@ -188,7 +188,7 @@ def test_wire_scenario_on_hip_engine(ntok):
 def run_probe(server: Path, keys: int, calls: int) -> dict:
     import json
     import sys
-    r = subprocess.run([sys.executable, str(ROOT / "backburner_amd" / "integration" / "serve_probe.py"), "--server", str(server),
+    r = subprocess.run([sys.executable, str(ROOT / "tests" / "serve_probe.py"), "--server", str(server),
                         "--keys", str(keys), "--calls", str(calls)], capture_output=True, text=True, timeout=300,
                        env=dict(os.environ, PA_GPU_MIN_KEYS="0"))
     assert r.returncode == 0, r.stdout + r.stderr
