@@ -14,12 +14,12 @@
 // Q' is the query as fp16: PA_QMODE_GGML converts Q to K's vec_dot type as ggml's CPU flash_attn_ext does - q8_0 per
 // 32-block for quantized K (quantize_row_q8_0_ref), taken as fp16(d*q*scale*log2 e) so the scores come out in base-2
 // units, and fp16(q) for f16 K (the scale then multiplies the score); PA_QMODE_F16 takes fp16(q*scale) (the reference
-// engines' Qs, phone-attn.h:595-599). Calls of up to 128 rows per KV head (4-wave workgroups) over quantized K in the
-// ggml rounding take exact block dots instead (EX below): K staged as its integer quants, three MFMAs per 32-dim
-// block, ggml's per-block scaling in fp32. Online softmax in base 2 with a reference max that moves only when a score
-// exceeds it by more than 2^MM_PMAX (O is rescaled rarely); the exact max is tracked beside it and applied at the end.
-// The row sum adds the fp16 probabilities the PV MFMAs consume. Output: one split-K slot per workgroup (O unnormalised against the
-// base-2 max, max, sum), folded by merge_kernel, or the final (O, m, l) when the call has a single chunk.
+// engines' Qs, phone-attn.h:595-599). Calls over quantized K in the ggml rounding take exact block dots instead (EX
+// below): K staged as its integer quants, three MFMAs per 32-dim block, ggml's per-block scaling in fp32. Online
+// softmax in base 2 with a reference max that moves only when a score exceeds it by more than 2^MM_PMAX (O is rescaled
+// rarely); the exact max is tracked beside it and applied at the end. The row sum adds the fp16 probabilities the PV
+// MFMAs consume. Output: one split-K slot per workgroup (O unnormalised against the base-2 max, max, sum), folded by
+// merge_kernel, or the final (O, m, l) when the call has a single chunk.
 //
 // Reference roles: pa_attn_big + pa_big_load (pa-metal.mm:379-487: per (row tile, KV head, key chunk) dequantize a
 // K/V block into threadgroup memory as half, S = QK^T on the matrix units, online softmax with key masking, O = a O +
@@ -374,8 +374,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     mm_write_out(a, O, mref, mx, lsum, h, row, rlive, h2, c);
 }
 
-// Up to 128 rows per KV head (4 waves: verify blocks, short calls) the ggml query rounding takes the exact block dots;
-// prefill chunks (8 waves) take the fp16-operand QK, which the prefill chunk's design specifies (K dequantized to fp16)
+// The ggml query rounding over quantized K takes the exact block dots at every size (4-wave verify blocks and 8-wave
+// prefill chunks); the reference engines' rounding (PA_QMODE_F16) and f16 K take the fp16-operand QK, the Metal
+// engine's own arithmetic (K dequantized to half in threadgroup memory, pa-metal.mm:379-487)
 template <int FMT, bool PRE>
 static hipError_t launch_mma_fmt(int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0,
                                  hipEvent_t ev1) {
@@ -385,8 +386,8 @@ static hipError_t launch_mma_fmt(int nw, bool skip, const AttnArgs & a, uint32_t
             else hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, false, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
             break;
         case 8:
-            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, true, false>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
-            else hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, false, false>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, true, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            else hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, false, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
             break;
         default: return hipErrorInvalidValue;
     }

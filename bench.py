@@ -16,9 +16,11 @@ Printed: ONE JSON line.
   cpu_baseline  the CPU path (oracle/pa_cpu_simd.c: ggml's CPU flash-attention arithmetic for q8_0 / q4_0, vectorized
               with AVX-512 VNNI or AVX2, equal to the oracle bit for bit) timed on this host's cores over a bounded sample
               of the workload, with the GPU's layer-0 output checked against it (parity_vs_cpu);
-  prefill     the 512-token prefill chunk (4,096 rows per KV head, 65,536 q8_0 keys, 64 distinct caches): us/layer,
-              TFLOP/s and the fraction of fp16 MFMA nameplate, counters from profiles/prefill_pmc.json, CPU leg over one
-              layer at full size;
+  prefill     the 512-token prefill chunk (4,096 rows per KV head, 65,536 q8_0 keys, 64 distinct caches) in ggml's
+              rounding (exact integer block dots for QK): us/layer, TFLOP/s and the fraction of fp16 MFMA nameplate,
+              counters from profiles/prefill_pmc.json, CPU leg over one layer at full size;
+  prefill_f16 the same chunk in the reference engines' rounding (queries f16(q*scale), K/V dequantized to fp16 in LDS:
+              the Metal engine's arithmetic), no CPU leg (the CPU path is ggml's);
   verify      the 16-token verify block (1,024 rows over 98,304 q8_0 keys, 64 layers): GB/s and the fraction of HBM
               nameplate, traffic from profiles/verify_pmc.json, CPU leg;
   decode_q4_0, verify_q4_0, decode_4096, accept   the 4-bit cache (143,360 positions), the 4,096-key decode layer of
@@ -346,8 +348,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=64)
-    ap.add_argument("--only", default="", help="comma list of the extra workloads to run (prefill, verify, decode_q4_0, "
-                                                "verify_q4_0, decode_4096, reference_shape, accept); default all")
+    ap.add_argument("--only", default="", help="comma list of the extra workloads to run (prefill, prefill_f16, verify, "
+                                                "decode_q4_0, verify_q4_0, decode_4096, reference_shape, accept); default all")
     ap.add_argument("--secondary", action="store_true", help="also run the reply side, KV ingest and the head-dim-256 shape")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-layers", type=int, default=16, help="layers of the headline workload the CPU baseline runs")
@@ -382,8 +384,15 @@ def main():
         extra["prefill"] = workload(
             bb, ws, args, "prefill", bb.FMT_Q8_0, nl, 65536, 4096,
             f"prefill chunk: 512 tokens x 64 q-heads / 8 kv-heads (4096 rows per KV head), hd 128, 65536 q8_0 keys, "
-            f"{nl} distinct caches", "mfma", "pa_hip::mma_kernel<1, 8, true, false, false> (q8_0 prefill, fp16 QK)",
+            f"{nl} distinct caches", "mfma", "pa_hip::mma_kernel<1, 8, true, false, true> (q8_0 prefill, exact block dots)",
             max(1, min(args.steps, 3)), 1, pmc="prefill", outliers=0)
+    if want("prefill_f16"):
+        extra["prefill_f16"] = workload(
+            bb, ws, args, "prefill_f16", bb.FMT_Q8_0, nl, 65536, 4096,
+            f"prefill chunk as above in the reference engines' rounding: queries f16(q*scale), K/V dequantized to fp16 in "
+            f"LDS, fp16 MFMA with fp32 accumulation (the Metal engine's arithmetic), {nl} distinct caches", "mfma",
+            "pa_hip::mma_kernel<1, 8, false, false, false> (q8_0 prefill, fp16 operands)",
+            max(1, min(args.steps, 3)), 0, pmc="prefill_f16", outliers=0, qmode=bb.QMODE_F16)
     if want("verify"):
         extra["verify"] = workload(
             bb, ws, args, "verify", bb.FMT_Q8_0, nl, 98304, 128,

@@ -5,7 +5,8 @@ O, m and l; orc_attn_ggml in PA_QMODE_GGML):
   groups of two tiles per head pair, then the wide merge;
 - the prefill chunk at full size (8 KV heads x 4,096 rows x 65,536 q8_0 keys, 16 pages), the geometry the benchmark
   times (8 heads x 16 row blocks x 2 key chunks, then the few-slot merge), checked on every 16th row of every head and
-  row block at all keys, with plain and with x8 outlier-channel keys;
+  row block at all keys, with plain and with x8 outlier-channel keys, and in the reference engines' rounding
+  (f16 queries, fp16-dequantized K/V) against the fp64 form;
 - the 16-token verify at 98,304 keys with x8 outlier-channel keys;
 - more than 256 split-K slots (a decode over 65 pages: two launches, 272 slots, the generic merge);
 - pages whose byte size exceeds 2^32 (rows of 4,352 bytes, 2^20 + 100 keys), through the decode and the matrix-core
@@ -102,27 +103,35 @@ def test_decode_4096_one_page(ws):
         c.close()
 
 
-# The prefill kernel computes QK on fp16 matrix cores over fp16-dequantized K and an fp16 query (the design the prefill
-# chunk is specified with: K/V dequantized to fp16 in LDS, fp32 accumulation), two roundings of 2^-11 that exact
-# integer block dots do not have. On the prefill workload's N(0,1) keys that stays inside the 2e-3 bar. Keys with x8
-# outlier channels (the decode workload's stress) make |q.k| larger and with it the logit error of those roundings:
-# that case is held to 5e-3, the reference's own gate for its fp16 GPU engine against the fp64 form
-# (phone-attn/pa-tool.cpp:173).
-PREFILL_OUTLIER_TOL = 5e-3
-
-
 @pytest.mark.parametrize("outliers", [0, 4])
 def test_prefill_full_size_sampled_rows(ws, outliers):
     """The prefill chunk as the benchmark runs it: 8 KV heads x 4,096 rows (512 tokens x GQA 8) x 65,536 q8_0 keys in 16
     pages; every 16th row of each head (offset 5, so every row block and every wave's row range is sampled) against the
-    oracle at all keys. Plain N(0,1) keys at the 2e-3 bar; x8 outlier-channel keys at 5e-3 (see above)."""
+    oracle at all keys, plain N(0,1) keys and x8 outlier-channel keys, both at the 2e-3 bar (exact integer block dots
+    for QK, as ggml computes them)."""
     print(f"prefill full size, outliers={outliers}", flush=True)
     c = DevCase(bb.FMT_Q8_0, 8, 4096, 65536, 4201 + outliers, outliers=outliers)
     try:
         out = c.run(ws)
         sel = np.arange(5, 4096, 16)
-        check(f"prefill 65536 outliers={outliers} (rows {len(sel)} of 4096 per head)", pick(out, 8, 4096, sel), c.oracle(sel),
-              tol=TOL if outliers == 0 else PREFILL_OUTLIER_TOL)
+        check(f"prefill 65536 outliers={outliers} (rows {len(sel)} of 4096 per head)", pick(out, 8, 4096, sel), c.oracle(sel))
+    finally:
+        c.close()
+
+
+def test_prefill_full_size_reference_rounding(ws):
+    """The same chunk in the reference engines' rounding (PA_QMODE_F16: queries f16(q*scale), K/V dequantized to fp16
+    in LDS, fp16 MFMA with fp32 accumulation - the Metal engine's arithmetic, pa-metal.mm:379-487) on N(0,1) keys:
+    every 64th row of each head (offset 9) against the fp64 closed form with the same query rounding, at 2e-3."""
+    print("prefill full size, reference rounding", flush=True)
+    c = DevCase(bb.FMT_Q8_0, 8, 4096, 65536, 4301)
+    try:
+        out = c.run(ws, qmode=bb.QMODE_F16)
+        sel = np.arange(9, 4096, 64)
+        Q = c.Q.reshape(8, 4096, 128)[:, sel, :].reshape(-1, 128)
+        ref = orc.attn_exact(orc.make_shape(8, len(sel), 128, orc.Q8_0, orc.QMODE_F16, rs=c.rs), Q,
+                             c.kbuf.download(np.uint8), c.vbuf.download(np.uint8), c.nk)
+        check(f"prefill 65536 reference rounding (rows {len(sel)} of 4096 per head)", pick(out, 8, 4096, sel), ref)
     finally:
         c.close()
 
