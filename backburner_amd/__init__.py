@@ -95,6 +95,10 @@ def lib() -> C.CDLL:
     L.pa_hip_accept.argtypes = [vp, vp, C.c_int, C.c_int64, vp, vp, vp]
     L.pa_hip_ws_set_split.restype = C.c_int
     L.pa_hip_ws_set_split.argtypes = [vp, C.c_int, C.c_int]
+    L.pa_hip_ws_set_chunk_keys.restype = C.c_int
+    L.pa_hip_ws_set_chunk_keys.argtypes = [vp, C.c_uint32]
+    L.pa_hip_warm.restype = C.c_int
+    L.pa_hip_warm.argtypes = [vp]
     L.pa_hip_ws_time_next.restype = C.c_int
     L.pa_hip_ws_time_next.argtypes = [vp, vp, vp]
     L.pa_hip_quantize.restype = C.c_int
@@ -314,6 +318,10 @@ class Workspace:
     def set_split(self, decode_groups: int = 0, mma_workgroups: int = 0) -> None:
         """pa_hip_ws_set_split: force the split-K geometry of this workspace's calls (0 = default)."""
         _check(lib().pa_hip_ws_set_split(self.ptr, decode_groups, mma_workgroups), "pa_hip_ws_set_split")
+
+    def set_chunk_keys(self, keys: int = 0) -> None:
+        """pa_hip_ws_set_chunk_keys: about `keys` keys per workgroup's split-K chunk (config_req.gpu_chunk; 0 = default)."""
+        _check(lib().pa_hip_ws_set_chunk_keys(self.ptr, keys), "pa_hip_ws_set_chunk_keys")
 
     def time_next(self, ev_start, ev_end) -> None:
         """Record ev_start / ev_end around the attention kernel of the next attn() call."""

@@ -74,8 +74,9 @@ struct pa_hip_ws {
     // buffers replaced by a larger one: a graph captured earlier may still name them, so they live as long as the
     // workspace (growth at least doubles a buffer, so they hold less than the live ones)
     std::vector<void *> retired;
-    // split-K geometry overrides (pa_hip_ws_set_split); 0 = the default geometry
+    // split-K geometry overrides (pa_hip_ws_set_split, pa_hip_ws_set_chunk_keys); 0 = the default geometry
     int dec_groups = 0, mma_workgroups = 0;
+    uint32_t chunk_keys = 0;
     // the sme_* compatibility path: its own stream, device staging and a pinned host staging area (host rows are copied
     // into it on the calling thread, so every transfer is pinned <-> device); `broken` after a call whose wait timed
     // out (its transfers may still land in the staging areas, so the workspace is not used again)
@@ -164,6 +165,12 @@ extern "C" int pa_hip_ws_set_split(pa_hip_ws * ws, int decode_groups, int mma_wo
     return 0;
 }
 
+extern "C" int pa_hip_ws_set_chunk_keys(pa_hip_ws * ws, uint32_t keys) {
+    if (!ws) { set_err("pa_hip_ws_set_chunk_keys: null workspace"); return -1; }
+    ws->chunk_keys = keys;
+    return 0;
+}
+
 extern "C" int pa_hip_alloc_page(size_t bytes, void ** k, void ** v) {
     if (!k || !v) { set_err("pa_hip_alloc_page: null output"); return -1; }
     *k = *v = nullptr;
@@ -194,6 +201,7 @@ struct Call {
     char * fixed = nullptr;           // ... or in a fixed device array of `cap` bytes (nothing allocated)
     size_t cap = 0;
     int dec_groups = 0, mma_workgroups = 0;
+    uint32_t chunk_keys = 0;          // keys per workgroup's chunk (config_req.gpu_chunk); 0 = the default geometry
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     uint16_t * reply_oh = nullptr;
     float * reply_lse = nullptr;
@@ -278,6 +286,7 @@ int attn_decode(Call & cx, const pa_hip_shape * s, const void * const * k_pages,
     auto groups = [&](uint64_t tiles, uint64_t cap) {
         const uint64_t target = s->fmt == PA_FMT_Q4_0 ? DEC_TARGET_WG_Q4 : DEC_TARGET_WG_Q8;
         const uint64_t want = cx.dec_groups > 0 ? (uint64_t) cx.dec_groups
+                            : cx.chunk_keys > 0 ? (tiles + std::max<uint64_t>(1, cx.chunk_keys / 32) - 1) / std::max<uint64_t>(1, cx.chunk_keys / 32)
                                                 : std::min<uint64_t>(std::max<uint64_t>(1, target / (s->nkv / 2)), (tiles + 1) / 2);
         return (uint32_t) std::max<uint64_t>(1, std::min({tiles, want, cap}));
     };
@@ -343,6 +352,9 @@ int attn_mma(Call & cx, const pa_hip_shape * s, const void * const * k_pages, co
     auto chunking = [&](uint64_t tiles, uint64_t cap, uint32_t & tpc) {
         const uint64_t want = std::max<uint64_t>(1, std::min(target / units, cap));
         tpc = (uint32_t) ((tiles + want - 1) / want);
+        if (cx.chunk_keys > 0 && cx.mma_workgroups == 0)             // keys per chunk asked for, within the slot cap
+            tpc = (uint32_t) std::max<uint64_t>((tiles + std::min(cap, tiles) - 1) / std::min(cap, tiles),
+                                                std::max<uint32_t>(1, cx.chunk_keys / 32));
         return (uint32_t) ((tiles + tpc - 1) / tpc);
     };
     uint32_t n_launch = 0, tpc = 0;
@@ -401,6 +413,8 @@ int attn_generic(Call & cx, const pa_hip_shape * s, const void * const * k_pages
     auto chunking = [&](uint64_t keys, uint64_t cap, uint32_t & chunk) {
         const uint64_t want = std::max<uint64_t>(1, std::min(target / units, cap));
         uint64_t c = (keys + want - 1) / want;
+        if (cx.chunk_keys > 0 && cx.mma_workgroups == 0)
+            c = std::max<uint64_t>((keys + std::min(cap, keys) - 1) / std::min(cap, keys), cx.chunk_keys);
         c = std::max<uint64_t>((uint64_t) nb, (c + nb - 1) / nb * nb);
         chunk = (uint32_t) c;
         return (uint32_t) ((keys + c - 1) / c);
@@ -533,7 +547,7 @@ extern "C" int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * s, const void * 
     if (!attn_args_ok("pa_hip_attn", s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l)) return -1;
     Call cx;
     cx.ws = ws;
-    cx.dec_groups = ws->dec_groups; cx.mma_workgroups = ws->mma_workgroups;
+    cx.dec_groups = ws->dec_groups; cx.mma_workgroups = ws->mma_workgroups; cx.chunk_keys = ws->chunk_keys;
     cx.ev0 = ws->ev0; cx.ev1 = ws->ev1;
     ws->ev0 = ws->ev1 = nullptr;
     return attn_call(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, (hipStream_t) stream);
@@ -571,7 +585,7 @@ extern "C" int pa_hip_attn_reply(pa_hip_ws * ws, const pa_hip_shape * s, const v
     if (!attn_args_ok("pa_hip_attn_reply", s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l)) return -1;
     Call cx;
     cx.ws = ws;
-    cx.dec_groups = ws->dec_groups; cx.mma_workgroups = ws->mma_workgroups;
+    cx.dec_groups = ws->dec_groups; cx.mma_workgroups = ws->mma_workgroups; cx.chunk_keys = ws->chunk_keys;
     cx.ev0 = ws->ev0; cx.ev1 = ws->ev1;
     ws->ev0 = ws->ev1 = nullptr;
     cx.reply_oh = Oh; cx.reply_lse = lse;

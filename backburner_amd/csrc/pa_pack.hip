@@ -7,7 +7,8 @@
 //   - for one group with 1 <= ntok < 8 real tokens, only the real rows (rows = (nr/8)*ntok, member k's token t at
 //     k*ntok + t), as the reference's Metal engine packs them (pa-metal.mm:630-634 geom, 661-672 pack_q).
 // pa_pack_q_kernel converts and places Q; pa_unpack_kernel places (O, m, l) back, giving the rows of tokens the call
-// did not have (0, -inf, 0): no keys (pa-metal.mm:501-505).
+// did not have (0, -inf, 0): no keys (pa-metal.mm:501-505). pa_warm_kernel is the server's keep-warm dispatch between
+// calls (the Metal engine's 32-thread warm dispatch, pa-metal.mm:955-968).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -90,7 +91,17 @@ bool launched(const char * fn) {
     return false;
 }
 
+// one wave that reads nothing and writes nothing: a dispatch that keeps the device's clocks up between calls
+__global__ __launch_bounds__(64) void pa_warm_kernel(uint32_t * sink, uint32_t v) {
+    if (sink && v == 0xffffffffu && threadIdx.x == 0) *sink = v;   // never true: the host passes a null sink
+}
+
 }  // namespace
+
+extern "C" int pa_hip_warm(void * stream) {
+    hipLaunchKernelGGL(pa_warm_kernel, dim3(1), dim3(64), 0, (hipStream_t) stream, (uint32_t *) nullptr, 0u);
+    return launched("pa_hip_warm") ? 0 : -1;
+}
 
 extern "C" int pa_hip_pack_q(const uint16_t * qs, uint32_t ng, uint32_t nkv, uint32_t nr, uint32_t hd, uint32_t ntok,
                              float * q, void * stream) {

@@ -50,6 +50,7 @@ struct hip_engine : pa::engine {
     }
     ~hip_engine() override {
         if (st_ && !idle(wait_ms())) return;   // work still in flight after the limit: leave its buffers to the process
+        disarm();
         if (ws_) pa_hip_ws_destroy(ws_);
         (void) hipFree(dbuf_);
         (void) hipHostFree(hbuf_);
@@ -73,6 +74,10 @@ struct hip_engine : pa::engine {
     }
     void free_page(pa::page & p) override {
         if (!idle(wait_ms())) { p = pa::page(); return; }            // a copy of this page may be in flight: leak it
+        {
+            std::lock_guard<std::mutex> lk(gate_mu_);
+            disarm();                                                // it may name this page
+        }
         {
             std::lock_guard<std::mutex> lk(mu_);
             held_.erase(p.hk);
@@ -112,43 +117,131 @@ struct hip_engine : pa::engine {
     double exec_ms() const override { return last_ms_; }
     std::string describe() override {
         return "hip MI355X (libpa_hip) rows_uploaded=" + std::to_string(rows_up_) + (tracked_ ? " tracked=1" : " tracked=0") +
-               " call_rows_per_kv_head=" + std::to_string(last_rows_);
+               " call_rows_per_kv_head=" + std::to_string(last_rows_) + " armed=" + std::to_string(n_armed_) +
+               " armed_hits=" + std::to_string(n_armed_hits_) + " warms=" + std::to_string(n_warm_);
     }
     uint64_t rows_uploaded() const { return rows_up_; }   // K/V rows copied to HBM since init
+    uint64_t armed_hits() const { return n_armed_hits_; }  // calls that ran as an armed graph
+
+    // between calls (the server's hot spin, phone-attn.h:356-370): one small dispatch, not waited for, so the device
+    // keeps its clocks up; skipped while a call is in flight (as the Metal engine skips it, pa-metal.mm:955-968)
+    void warm() override {
+        std::lock_guard<std::mutex> lk(gate_mu_);
+        if (closing_ || in_call_) return;
+        if (pa_hip_warm(st_) == 0) n_warm_++;
+    }
+
+    // after a one-group call the server names the likely next call (the next layer, same split and tokens,
+    // phone-attn.h:687-697): its whole launch sequence (query copy, packing, attention, unpacking, reply copy) is
+    // captured now as a HIP graph, off the critical path, so that the call itself is one memcpy of Q into pinned memory
+    // and one graph launch (the Metal engine's pre-encoded command buffer, pa-metal.mm:716-765). A call that does not
+    // match it (other pages, key counts, tokens or row format) runs the ordinary launches. Off unless PA_GPU_ARM=1, as
+    // in the Metal engine: at 131,072 keys, back-to-back decode calls over loopback measured 0.479 ms per round trip
+    // armed against 0.446 ms not (the capture and instantiation run on the server thread after the reply, when a fast
+    // client's next call is already waiting).
+    void arm(const pa::page * pages, const uint32_t * nkeys, int n_pages, const pa::config_req & cfg, int ntok) override {
+        static const bool on = getenv("PA_GPU_ARM") && atoi(getenv("PA_GPU_ARM")) != 0;
+        std::lock_guard<std::mutex> lk(gate_mu_);
+        disarm();
+        if (!on || closing_ || in_call_ || n_pages <= 0) return;
+        const call_geom g = geom_of(cfg, 1, ntok);
+        if (!ensure(g.dev_bytes(), g.host_bytes())) return;
+        (void) pa_hip_ws_set_chunk_keys(ws_, cfg.gpu_chunk);
+        if (hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal) != hipSuccess) { (void) hipGetLastError(); return; }
+        const bool ok = enqueue(pages, nkeys, n_pages, cfg, g, false);
+        hipGraph_t graph = nullptr;
+        const bool ended = hipStreamEndCapture(st_, &graph) == hipSuccess;
+        if (ok && ended && graph && hipGraphInstantiate(&armed_.exec, graph, nullptr, nullptr, 0) == hipSuccess) {
+            armed_.hk.resize(n_pages); armed_.nkeys.assign(nkeys, nkeys + n_pages);
+            for (int i = 0; i < n_pages; i++) armed_.hk[i] = pages[i].hk;
+            armed_.rs = cfg.rs; armed_.hb = cfg.hb; armed_.is_q8 = cfg.is_q8; armed_.nkv = cfg.n_head_kv;
+            armed_.chunk = cfg.gpu_chunk; armed_.nt = g.nt;
+            n_armed_++;
+        } else {
+            armed_.exec = nullptr;
+            (void) hipGetLastError();
+        }
+        if (graph) (void) hipGraphDestroy(graph);
+    }
 
 private:
+    // one call's rows and buffer layout: device qs (f16, server layout) | Q (fp32, call layout) | O, m, l (call) |
+    // O, m, l (server); host (pinned): qs | O, m, l (server)
+    struct call_geom {
+        uint32_t nkv = 0, ng = 1, nt = 0, rows = 0;
+        size_t srows = 0, crows = 0, qs_b = 0, q_b = 0, oc_b = 0, os_b = 0;
+        size_t dev_bytes() const { return qs_b + q_b + oc_b + os_b; }
+        size_t host_bytes() const { return qs_b + os_b; }
+    };
+    static call_geom geom_of(const pa::config_req & cfg, int ng, int ntok) {
+        call_geom g;
+        g.nkv = (uint32_t) cfg.n_head_kv; g.ng = (uint32_t) ng;
+        g.nt = (ng == 1 && ntok >= 1 && ntok < 8) ? (uint32_t) ntok : 0;
+        g.rows = g.nt ? (pa::NR / 8) * g.nt : g.ng * pa::NR;                  // call rows per KV head
+        g.srows = (size_t) g.ng * g.nkv * pa::NR; g.crows = (size_t) g.nkv * g.rows;
+        g.qs_b = al(g.srows * pa::HD * 2); g.q_b = al(g.crows * pa::HD * 4); g.oc_b = al(g.crows * (pa::HD + 2) * 4);
+        g.os_b = al(g.srows * (pa::HD + 2) * 4);
+        return g;
+    }
+
     bool start(const pa::page * pages, const uint32_t * nkeys, int n_pages, const uint16_t * Qs, const pa::config_req & cfg,
                int ng) {
-        nkv_ = (uint32_t) cfg.n_head_kv; ng_ = (uint32_t) ng;
-        nt_ = (ng == 1 && ntok_hint >= 1 && ntok_hint < 8) ? (uint32_t) ntok_hint : 0;
-        const uint32_t rows = nt_ ? (pa::NR / 8) * nt_ : ng_ * pa::NR;          // call rows per KV head
-        last_rows_ = rows;
-        const size_t srows = (size_t) ng_ * nkv_ * pa::NR, crows = (size_t) nkv_ * rows;
-        // device: qs (f16, server layout) | Q (fp32, call layout) | O, m, l (call) | O, m, l (server); host: qs | O, m, l
-        const size_t qs_b = al(srows * pa::HD * 2), q_b = al(crows * pa::HD * 4), oc_b = al(crows * (pa::HD + 2) * 4);
-        const size_t os_b = al(srows * (pa::HD + 2) * 4);
-        if (!ensure(qs_b + q_b + oc_b + os_b, qs_b + os_b)) return false;
+        const call_geom g = geom_of(cfg, ng, ntok_hint);
+        nkv_ = g.nkv; ng_ = g.ng; nt_ = g.nt; last_rows_ = g.rows;
+        const bool hit = armed_match(pages, nkeys, n_pages, cfg, ng, g.nt);
+        if (!hit) disarm();
+        if (!ensure(g.dev_bytes(), g.host_bytes())) return false;
         if (!upload_rows(pages, nkeys, n_pages, cfg.rs)) return false;
+        std::memcpy(hbuf_, Qs, g.srows * pa::HD * 2);
+        hout_ = (const float *) (hbuf_ + g.qs_b);
+        if (hit) {                                                   // the armed launch sequence, timed as a whole
+            const bool ok = hipEventRecord(e0_, st_) == hipSuccess && hipGraphLaunch(armed_.exec, st_) == hipSuccess &&
+                            hipEventRecord(e1_, st_) == hipSuccess;
+            disarm();
+            if (!ok) return fail("armed graph launch");
+            n_armed_hits_++;
+            return true;
+        }
+        (void) pa_hip_ws_set_chunk_keys(ws_, cfg.gpu_chunk);
+        return enqueue(pages, nkeys, n_pages, cfg, g, true);
+    }
+
+    // the call's launch sequence on the engine stream (the query is in hbuf_); `timed` records e0 / e1 around the
+    // attention (not inside a capture: the armed path times its whole graph instead)
+    bool enqueue(const pa::page * pages, const uint32_t * nkeys, int n_pages, const pa::config_req & cfg, const call_geom & g,
+                 bool timed) {
         char * d = dbuf_;
-        uint16_t * dqs = (uint16_t *) d; float * dq = (float *) (d + qs_b);
-        float * dO = (float *) (d + qs_b + q_b), * dm = dO + crows * pa::HD, * dl = dm + crows;
-        float * sO = (float *) (d + qs_b + q_b + oc_b), * sm = sO + srows * pa::HD, * sl = sm + srows;
-        std::memcpy(hbuf_, Qs, srows * pa::HD * 2);
-        if (hipMemcpyAsync(dqs, hbuf_, srows * pa::HD * 2, hipMemcpyHostToDevice, st_) != hipSuccess) return fail("Q upload");
-        if (pa_hip_pack_q(dqs, ng_, nkv_, pa::NR, pa::HD, nt_, dq, st_) != 0) return fail(std::string("pa_hip_pack_q: ") + pa_hip_last_error());
+        uint16_t * dqs = (uint16_t *) d; float * dq = (float *) (d + g.qs_b);
+        float * dO = (float *) (d + g.qs_b + g.q_b), * dm = dO + g.crows * pa::HD, * dl = dm + g.crows;
+        float * sO = (float *) (d + g.qs_b + g.q_b + g.oc_b), * sm = sO + g.srows * pa::HD, * sl = sm + g.srows;
+        if (hipMemcpyAsync(dqs, hbuf_, g.srows * pa::HD * 2, hipMemcpyHostToDevice, st_) != hipSuccess) return fail("Q upload");
+        if (pa_hip_pack_q(dqs, g.ng, g.nkv, pa::NR, pa::HD, g.nt, dq, st_) != 0) return fail(std::string("pa_hip_pack_q: ") + pa_hip_last_error());
         std::vector<const void *> kp(n_pages), vp(n_pages);
         for (int i = 0; i < n_pages; i++) { kp[i] = pages[i].hk; vp[i] = pages[i].hv; }
-        const pa_hip_shape s = {nkv_, rows, (uint32_t) pa::HD, cfg.is_q8, cfg.rs, cfg.hb, PA_QMODE_F16, 1.0f};
-        if (hipEventRecord(e0_, st_) != hipSuccess) return fail("event");
+        const pa_hip_shape s = {g.nkv, g.rows, (uint32_t) pa::HD, cfg.is_q8, cfg.rs, cfg.hb, PA_QMODE_F16, 1.0f};
+        if (timed && hipEventRecord(e0_, st_) != hipSuccess) return fail("event");
         if (pa_hip_attn(ws_, &s, kp.data(), vp.data(), nkeys, n_pages, dq, dO, dm, dl, st_) != 0)
             return fail(std::string("pa_hip_attn: ") + pa_hip_last_error());
-        if (hipEventRecord(e1_, st_) != hipSuccess) return fail("event");
-        if (pa_hip_unpack_rows(dO, dm, dl, ng_, nkv_, pa::NR, pa::HD, nt_, sO, sm, sl, st_) != 0)
+        if (timed && hipEventRecord(e1_, st_) != hipSuccess) return fail("event");
+        if (pa_hip_unpack_rows(dO, dm, dl, g.ng, g.nkv, pa::NR, pa::HD, g.nt, sO, sm, sl, st_) != 0)
             return fail(std::string("pa_hip_unpack_rows: ") + pa_hip_last_error());
-        if (hipMemcpyAsync(hbuf_ + qs_b, sO, srows * (pa::HD + 2) * 4, hipMemcpyDeviceToHost, st_) != hipSuccess)
+        if (hipMemcpyAsync(hbuf_ + g.qs_b, sO, g.srows * (pa::HD + 2) * 4, hipMemcpyDeviceToHost, st_) != hipSuccess)
             return fail("O download");
-        hout_ = (const float *) (hbuf_ + qs_b);
         return true;
+    }
+
+    // the armed graph is for exactly these pages, key counts, tokens and row format, one group
+    bool armed_match(const pa::page * pages, const uint32_t * nkeys, int n_pages, const pa::config_req & cfg, int ng,
+                     uint32_t nt) const {
+        if (!armed_.exec || ng != 1 || (int) armed_.hk.size() != n_pages || armed_.nt != nt || armed_.rs != cfg.rs ||
+            armed_.hb != cfg.hb || armed_.is_q8 != cfg.is_q8 || armed_.nkv != cfg.n_head_kv || armed_.chunk != cfg.gpu_chunk)
+            return false;
+        for (int i = 0; i < n_pages; i++) if (armed_.hk[i] != pages[i].hk || armed_.nkeys[i] != nkeys[i]) return false;
+        return true;
+    }
+    void disarm() {
+        if (armed_.exec) (void) hipGraphExecDestroy(armed_.exec);
+        armed_ = armed_t();
     }
 
     double finish(float * O, float * m, float * l) {
@@ -231,6 +324,7 @@ private:
     bool ensure(size_t dev_b, size_t host_b) {
         if (dev_b <= dcap_ && host_b <= hcap_) return true;
         if (!idle(wait_ms())) return false;
+        disarm();                                                    // it names the buffers freed here
         (void) hipFree(dbuf_); (void) hipHostFree(hbuf_);
         dbuf_ = nullptr; hbuf_ = nullptr; dcap_ = hcap_ = 0;
         if (hipMalloc((void **) &dbuf_, dev_b) != hipSuccess) return fail("hipMalloc call buffers");
@@ -251,6 +345,13 @@ private:
     tracker tracker_;
     std::mutex mu_;
     std::unordered_map<void *, held> held_;   // per page (keyed by its HBM K copy)
+    struct armed_t {                          // the graph arm() captured, and the call it is for
+        hipGraphExec_t exec = nullptr;
+        std::vector<void *> hk;
+        std::vector<uint32_t> nkeys;
+        uint32_t rs = 0, hb = 0, is_q8 = 0, nkv = 0, chunk = 0, nt = 0;
+    } armed_;
+    uint64_t n_armed_ = 0, n_armed_hits_ = 0, n_warm_ = 0;
     std::mutex gate_mu_;                      // close(): no call in flight, none started after it
     std::condition_variable gate_cv_;
     bool closing_ = false, in_call_ = false;

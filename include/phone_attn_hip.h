@@ -110,6 +110,12 @@ void pa_hip_ws_destroy(pa_hip_ws * ws);
  * default (about 1024 decode workgroups, one round of resident workgroups otherwise). Returns 0 or -1. */
 int pa_hip_ws_set_split(pa_hip_ws * ws, int decode_groups, int mma_workgroups);
 
+/* config_req.gpu_chunk (phone-attn.h:88-89, "keys per GPU threadgroup"; the Metal engine's chunk, pa-metal.mm:842): each
+ * workgroup of this workspace's calls takes a split-K chunk of about `keys` keys (rounded to the kernel's 32-key tiles,
+ * or to the head-dim-256 generic kernel's key block); 0 restores the default geometry. pa_hip_ws_set_split's counts, when
+ * set, take precedence. Returns 0 or -1. */
+int pa_hip_ws_set_chunk_keys(pa_hip_ws * ws, uint32_t keys);
+
 /* engine::alloc_page / free_page (phone-attn.h:168-169): K and V storage of one page in HBM (device pointers, 256-byte
  * aligned). Returns 0 or -1. */
 int pa_hip_alloc_page(size_t bytes, void ** k, void ** v);
@@ -204,6 +210,10 @@ int pa_hip_quantize(int fmt, const float * x, void * y, int64_t n, void * stream
  * memory). Returns 0 once enqueued, -1 on a bad argument. */
 int pa_hip_pack_q(const uint16_t * qs, uint32_t ng, uint32_t nkv, uint32_t nr, uint32_t hd, uint32_t ntok, float * q,
                   void * stream);
+/* The server's keep-warm dispatch between calls (pa::engine::warm, phone-attn.h:179; the Metal engine's 32-thread dispatch,
+ * pa-metal.mm:955-968): one 64-thread workgroup that does no work, enqueued on `stream` and not waited for. Returns 0,
+ * or -1 if the launch failed. */
+int pa_hip_warm(void * stream);
 /* The way back: a call's (O, m, l) [nkv][rows] (rows as pa_hip_pack_q made them) to the server's rows Os [ng][nkv*nr][hd],
  * ms, ls [ng][nkv*nr]; the rows of tokens the call did not have get (0, -inf, 0), no keys (pa-metal.mm:501-505). Device
  * pointers, O and Os 16-byte aligned. Returns 0 once enqueued, -1 on a bad argument. */

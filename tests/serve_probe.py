@@ -1,8 +1,10 @@
 """Drives pa-hip-serve (the reference's unchanged pa::server with the HIP engine) over the PATN wire at long context and
-prints one JSON line: the client's wall time per ATTN, the engine's GPU time per call, and how many K/V rows the engine
-uploaded to HBM - once when the first call reads the held pages, then only rows appended since.
+prints one JSON line: the client's wall time per ATTN, the engine's GPU time per call, how many K/V rows the engine
+uploaded to HBM - once when the first call reads the held pages, then only rows appended since - and how many calls
+ran as the engine's pre-armed graph (the server arms the next layer's call after each reply; with one layer that is
+the same layer's next call; the engine arms only with --arm, PA_GPU_ARM=1).
 
-    python3 tests/serve_probe.py [--keys 131072] [--calls 20] [--ntok 1] [--server PATH]
+    python3 tests/serve_probe.py [--keys 131072] [--calls 20] [--ntok 1] [--server PATH] [--arm]
 
 Layout: the reference's shape (4 KV heads, 48 query rows, head dim 256), q8_0 rows of random quants, one layer. The
 probe starts the server on a free loopback port, sends CONFIG, APPENDs the keys in messages of 4,096 rows, makes three
@@ -13,6 +15,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import os
 import signal
 import socket
 import subprocess
@@ -52,13 +55,15 @@ def main() -> int:
     ap.add_argument("--keys", type=int, default=131072)
     ap.add_argument("--calls", type=int, default=20)
     ap.add_argument("--ntok", type=int, default=1)
+    ap.add_argument("--arm", action="store_true", help="run the server with PA_GPU_ARM=1 (pre-armed calls)")
     args = ap.parse_args()
     if args.keys % 4096:
         print(json.dumps({"error": "--keys must be a multiple of 4096"}))
         return 2
     port = free_port()
     cmd = [args.server] + (["serve"] if Path(args.server).name.startswith("pa-tool") else []) + [str(port), "2"]
-    srv = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE)
+    env = dict(os.environ, PA_GPU_ARM="1" if args.arm else "0")
+    srv = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, env=env)
     try:
         for _ in range(600):
             try:
@@ -79,9 +84,10 @@ def main() -> int:
         q = (rng.standard_normal((1, NKV, NR, HD)) * 1.7).astype(np.float16)
         q[:, :, (np.arange(NR) % 8) >= args.ntok, :] = 0
         Q = q.view(np.uint16)
-        def rows_stat():                          # the HIP engine's count (None for a server without it)
+        def stat(key):                            # a count of the HIP engine's (None for a server without it)
             st = c.stats()
-            return int(st.split("rows_uploaded=")[1].split()[0]) if "rows_uploaded=" in st else None
+            return int(st.split(key + "=")[1].split()[0]) if key + "=" in st else None
+        rows_stat = lambda: stat("rows_uploaded")
         for _ in range(3):
             c.attn(0, args.ntok, 0, 1.0 / 16, Q)
         up_warm = rows_stat()
@@ -98,10 +104,11 @@ def main() -> int:
                 gpu.append(rep["gpu_ms"])
             return wall, gpu
 
+        hits0 = stat("armed_hits")
         wall_h, gpu_h = timed(args.calls, False)
-        up_held = rows_stat()
+        up_held, hits_held = rows_stat(), stat("armed_hits")
         wall_a, gpu_a = timed(args.calls, True)
-        up_end = rows_stat()
+        up_end, hits_end = rows_stat(), stat("armed_hits")
         stats = c.stats()
         c.close()
         med = lambda v: round(float(np.median(v)), 4)
@@ -113,6 +120,7 @@ def main() -> int:
             "rows_uploaded": {"after_warmup": up_warm, "after_held_calls": up_held, "after_append_calls": up_end},
             "rows_uploaded_per_held_call": None if up_warm is None else (up_held - up_warm) / args.calls,
             "rows_uploaded_per_append_call": None if up_warm is None else (up_end - up_held) / args.calls,
+            "armed_calls": None if hits0 is None else {"held": hits_held - hits0, "append64": hits_end - hits_held},
             "server_stats": stats}), flush=True)
         return 0
     finally:

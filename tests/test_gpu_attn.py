@@ -177,6 +177,29 @@ def test_mma_split_invariance(ws, fmt, rows):
         assert eo < 1e-3 and em < 1e-6 and el < 2.0 ** -11, (eo, em, el)
 
 
+@pytest.mark.parametrize("fmt,rows,hd,qmode", [(bb.FMT_Q8_0, 8, 128, bb.QMODE_GGML), (bb.FMT_Q4_0, 128, 128, bb.QMODE_GGML),
+                                               (bb.FMT_Q8_0, 48, 256, bb.QMODE_F16), (bb.FMT_Q8_0, 48, 256, bb.QMODE_GGML)])
+@pytest.mark.parametrize("chunk", [64, 1000, 4096])
+def test_chunk_keys(ws, fmt, rows, hd, qmode, chunk):
+    """config_req.gpu_chunk (keys per workgroup, pa_hip_ws_set_chunk_keys) on the decode, verify, head-dim-256 matrix-core
+    and head-dim-256 generic kernels: every chunking within the parity bar of the oracle."""
+    nkv, nk = 2, 5000
+    print(f"chunk keys {chunk}: fmt={fmt} rows={rows} hd={hd} qmode={qmode}", flush=True)
+    K, V, Q, rs = case(fmt, nkv, rows, hd, nk, 1200 + chunk + rows)
+    shape = bb.make_shape(nkv, rows, hd, fmt, qmode, rs=rs)
+    if qmode == bb.QMODE_GGML:
+        ref = orc.attn_ggml(orc.make_shape(nkv, rows, hd, fmt, orc.QMODE_GGML, rs=rs), Q, K, V, nk)
+    else:
+        ref = orc.attn_exact(orc.make_shape(nkv, rows, hd, fmt, orc.QMODE_F16, rs=rs), Q, K, V, nk)
+    ws.set_chunk_keys(chunk)
+    try:
+        out = bb.attn_host(shape, K, V, Q, page_keys=1500, ws=ws)
+    finally:
+        ws.set_chunk_keys(0)
+    eo, em, el = orc.rel_err(*out, *ref)
+    assert eo < TOL and em < TOL and el < TOL, (eo, em, el)
+
+
 def test_bad_arguments(ws):
     with pytest.raises(bb.PaHipError, match="hd must be"):
         bb.attn_host(bb.make_shape(1, 8, 64, bb.FMT_Q8_0), np.zeros(68, np.uint8), np.zeros(68, np.uint8),

@@ -35,11 +35,12 @@ TOL = 2e-3
 
 
 class Server:
-    def __init__(self, cmd: list):
+    def __init__(self, cmd: list, arm: bool = False):
         self.port = free_port()
         # PA_GPU_MIN_KEYS=0: one-group calls go to the GPU engine below the server's default 16,384 keys too
-        # (phone-attn.h:584-586), so these small layers exercise it
-        env = dict(os.environ, PA_GPU_MIN_KEYS="0")
+        # (phone-attn.h:584-586), so these small layers exercise it; PA_GPU_ARM=1: the engine arms the call the server
+        # names after each reply
+        env = dict(os.environ, PA_GPU_MIN_KEYS="0", PA_GPU_ARM="1" if arm else "0")
         self.p = subprocess.Popen([str(c) for c in cmd] + [str(self.port), "2"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                                   env=env)
         for _ in range(300):
@@ -100,11 +101,12 @@ def stat(c: Client, key: str) -> int:
     return int(m.group(1))
 
 
-def scenario(cmd: list, ntok: int, gpu: bool):
+def scenario(cmd: list, ntok: int, gpu: bool, arm: bool = False):
     """CONFIG 2 layers; APPEND 6144 keys per layer; ATTN twice; APPEND 64; ATTN; TRUNCATE to 5000 (inside page 1) and
     APPEND different rows back to 6208; ATTN; TRUNCATE to 3000 (page 1 dropped, inside page 0) and APPEND again;
-    ATTN; then a 16-token ATTN_BIG over the same rows."""
-    srv = Server(cmd)
+    ATTN; then a 16-token ATTN_BIG over the same rows. With arm, the first call is followed by a call of layer 1 (the
+    call the server arms after it, phone-attn.h:687-697), which runs as the engine's armed graph."""
+    srv = Server(cmd, arm)
     c = Client(srv.port)
     try:
         c.hello()
@@ -117,6 +119,8 @@ def scenario(cmd: list, ntok: int, gpu: bool):
                 c.append(L, p0, src[p0:p0 + 4096], vs[p0:p0 + 4096])
             if L == 0:
                 V0 = vs
+            else:
+                K1, V1 = src, vs
         K0 = held
         Q = queries(31, 1, ntok)
 
@@ -134,7 +138,14 @@ def scenario(cmd: list, ntok: int, gpu: bool):
             up = stat(c, "rows_uploaded")
             assert up == 6144 and stat(c, "tracked") == 1
             assert stat(c, "call_rows_per_kv_head") == (6 * ntok if ntok < 8 else 48)
-        attn("held rows again")
+        if arm:                          # armed after the first call; the layer's 6144 rows are uploaded by it
+            rep, O16, lse = c.attn(1, ntok, 0, SCALE, Q)
+            check_reply(f"layer 1 after layer 0 (armed) ntok={ntok}", O16, lse, Q, K1, V1, ntok, gpu)
+            assert stat(c, "armed_hits") == 1, c.stats()
+            up += 6144
+        attn("held rows again")          # armed after the layer-1 call when arm is set
+        if arm:
+            assert stat(c, "armed_hits") == 2, c.stats()
         if gpu:
             assert stat(c, "rows_uploaded") == up, "a call over held rows uploaded rows"
         extra_k, extra_v = rows(41, 64), rows(42, 64)
@@ -185,11 +196,19 @@ def test_wire_scenario_on_hip_engine(ntok):
     scenario([SERVE_HIP], ntok, gpu=True)
 
 
-def run_probe(server: Path, keys: int, calls: int) -> dict:
+@pytest.mark.gpu
+@needs_hip_server
+@pytest.mark.parametrize("ntok", [1, 8])
+def test_wire_scenario_armed(ntok):
+    print(f"pa-hip-serve scenario armed ntok={ntok}", flush=True)
+    scenario([SERVE_HIP], ntok, gpu=True, arm=True)
+
+
+def run_probe(server: Path, keys: int, calls: int, arm: bool = False) -> dict:
     import json
     import sys
     r = subprocess.run([sys.executable, str(ROOT / "tests" / "serve_probe.py"), "--server", str(server),
-                        "--keys", str(keys), "--calls", str(calls)], capture_output=True, text=True, timeout=300,
+                        "--keys", str(keys), "--calls", str(calls)] + (["--arm"] if arm else []), capture_output=True, text=True, timeout=300,
                        env=dict(os.environ, PA_GPU_MIN_KEYS="0"))
     assert r.returncode == 0, r.stdout + r.stderr
     return json.loads(r.stdout.strip().splitlines()[-1])
@@ -213,3 +232,17 @@ def test_serve_probe_on_hip_engine():
     assert out["rows_uploaded"]["after_warmup"] == 8192
     assert out["rows_uploaded_per_held_call"] == 0 and out["rows_uploaded_per_append_call"] == 64
     assert out["held"]["gpu_ms_p50"] > 0
+    assert out["armed_calls"] == {"held": 0, "append64": 0}, out["armed_calls"]
+
+
+@pytest.mark.gpu
+@needs_hip_server
+def test_serve_probe_armed_calls():
+    """PA_GPU_ARM=1: the server arms the next call after each reply (phone-attn.h:687-697), the engine captures it as a
+    HIP graph. Every held-row call (same pages and key counts as the call before) runs as that graph; after an APPEND
+    the last page's key count differs, so none does. (The probe checks no reply; test_wire_scenario_armed checks an
+    armed call's reply against the fp64 form.)"""
+    print("serve probe armed, 8192 keys", flush=True)
+    out = run_probe(SERVE_HIP, 8192, 4, arm=True)
+    assert out["armed_calls"] == {"held": 4, "append64": 0}, out["armed_calls"]
+    assert out["rows_uploaded_per_held_call"] == 0 and out["rows_uploaded_per_append_call"] == 64
