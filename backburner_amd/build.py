@@ -42,7 +42,7 @@ SRC_FLAGS = {"pa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-n
              "pa_mma.hip": ["-fno-honor-nans"], "pa_mma256.hip": ["-fno-honor-nans"]}
 
 LIBS = {
-    "libpa_hip.so": ["pa_attn.hip", "pa_decode.hip", "pa_mma.hip", "pa_mma256.hip", "pa_accept.hip", "pa_reply.hip", "pa_ingest.hip",
+    "libpa_hip.so": ["pa_merge.hip", "pa_decode.hip", "pa_mma.hip", "pa_mma256.hip", "pa_accept.hip", "pa_reply.hip", "pa_ingest.hip",
                      "pa_noalloc.hip", "pa_pack.hip", "pa_abi.cpp"],
     "libpa_synth.so": ["pa_synth.hip"],
 }

@@ -192,7 +192,6 @@ namespace {
 // per layer against 58.3-58.4 at four per CU; 64k and 256k keys alike; counts between them leave a partial second
 // round and are slower). q4_0, twice the work per byte: four per CU (45.4-46.4 against 49.5-50.2 us at three).
 constexpr int DEC_TARGET_WG_Q8 = 768, DEC_TARGET_WG_Q4 = 1024;
-constexpr int GEN_TARGET_WG = 256;    // head dim 256 kernel: one round of resident workgroups
 
 // One call of the engine path: where its split-K slots go, its geometry overrides, its timing events and, for
 // pa_hip_attn_reply, the reply target the merge writes instead of (O, m, l).
@@ -398,67 +397,6 @@ int attn_mma(Call & cx, const pa_hip_shape * s, const void * const * k_pages, co
     return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
 }
 
-// head dim 256 with ggml's q8_0 query rounding: attn_kernel over (key chunk, head, row block) items, chunks of
-// keys that may span pages, about GEN_TARGET_WG workgroups per launch, slot-major slots
-int attn_generic(Call & cx, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
-                 const uint32_t * nkeys, int n_pages, const float * Q, float * O, float * m, float * l, hipStream_t st) {
-    const int cfg = s->rows <= 16 ? CFG_DECODE : CFG_MID;
-    int rows_wg = 16, nb = 64;
-    cfg_geometry(cfg, rows_wg, nb);
-    const uint32_t nrb = (s->rows + rows_wg - 1) / rows_wg, qr = nrb * rows_wg;
-    const uint32_t units = s->nkv * nrb;
-    const uint64_t rows_per_slot = (uint64_t) s->nkv * qr;
-    // one round of resident workgroups (8 rows x 4 KV heads x 65k q8_0 keys: 82 us at 256, against 112 us at 1024)
-    const uint64_t target = cx.mma_workgroups > 0 ? (uint64_t) cx.mma_workgroups : (uint64_t) GEN_TARGET_WG;
-    auto chunking = [&](uint64_t keys, uint64_t cap, uint32_t & chunk) {
-        const uint64_t want = std::max<uint64_t>(1, std::min(target / units, cap));
-        uint64_t c = (keys + want - 1) / want;
-        if (cx.chunk_keys > 0 && cx.mma_workgroups == 0)
-            c = std::max<uint64_t>((keys + std::min(cap, keys) - 1) / std::min(cap, keys), cx.chunk_keys);
-        c = std::max<uint64_t>((uint64_t) nb, (c + nb - 1) / nb * nb);
-        chunk = (uint32_t) c;
-        return (uint32_t) ((keys + c - 1) / c);
-    };
-    uint32_t n_launch = 0, chunk = 0;
-    uint64_t n_slots = 0, cap = ~0ull;
-    for_launches(nkeys, n_pages, [&](int, int, uint64_t, uint64_t keys) { n_launch++; n_slots += chunking(keys, cap, chunk); });
-    if (cx.fixed && !(n_launch == 1 && n_slots == 1) && n_slots * rows_per_slot > cx.max_rows(s->hd)) {
-        cap = chunk_cap(cx, n_launch, rows_per_slot, s->hd);
-        if (cap == 0) { set_err("pa_hip_attn_noalloc: " + std::to_string(n_launch) + " launches need more slots than the scratch holds"); return -1; }
-        n_slots = 0;
-        for_launches(nkeys, n_pages, [&](int, int, uint64_t, uint64_t keys) { n_slots += chunking(keys, cap, chunk); });
-    }
-    const bool direct = n_launch == 1 && n_slots == 1;
-    if (!direct && !cx.slots(n_slots * rows_per_slot, s->hd, st)) return -1;
-    if (cx.ev0 && !hip_ok(hipEventRecord(cx.ev0, st), "hipEventRecord")) return -1;
-    uint32_t slot0 = 0;
-    bool ok = true;
-    for_launches(nkeys, n_pages, [&](int p0, int np, uint64_t, uint64_t keys) {
-        if (!ok) return;
-        const uint32_t nch = chunking(keys, cap, chunk);
-        AttnArgs a;
-        std::memset(&a, 0, sizeof a);
-        page_table(a, k_pages, v_pages, nkeys, p0, np);
-        a.n_chunks = nch; a.chunk = chunk;
-        a.n_items = nch * units;
-        a.rs = s->rs; a.hb = s->hb; a.nkv = s->nkv; a.rows = s->rows; a.qr = qr; a.nrb = nrb; a.slot0 = slot0;
-        a.qmode = s->qmode; a.fused = direct ? 1u : 0u; a.scale = s->scale;
-        a.s_mul = (s->qmode == PA_QMODE_GGML ? s->scale : 1.0f) * 1.4426950408889634f;
-        a.q = Q; a.po = cx.po; a.pml = cx.pml; a.O = O; a.m = m; a.l = l;
-        const uint32_t grid = (a.n_items + 7) / 8 * 8;
-        ok = hip_ok(launch_attention((int) s->hd, (int) s->fmt, cfg, a, grid, st), "attention launch");
-        slot0 += nch;
-    });
-    if (!ok) return -1;
-    if (cx.ev1 && !hip_ok(hipEventRecord(cx.ev1, st), "hipEventRecord")) return -1;   // the attention kernel alone
-    if (direct) return 0;
-    MergeArgs ma;
-    ma.po = cx.po; ma.pml = cx.pml; ma.O = O; ma.m = m; ma.l = l;
-    ma.n_slots = (uint32_t) n_slots; ma.nkv = s->nkv; ma.qr = qr; ma.rows = s->rows;
-    ma.sst = (uint64_t) s->nkv * qr; ma.rst = 1;                     // slot-major slots
-    return cx.merge(ma, (int) s->hd, st) ? 0 : -1;
-}
-
 // the argument checks every engine-path attention call shares; false (with the message set) on a bad argument
 // (the message strings are built on the error path only: a good call allocates nothing on the host either)
 bool attn_args_ok(const char * fn, const pa_hip_shape * s, const void * const * k_pages, const void * const * v_pages,
@@ -497,10 +435,8 @@ int attn_dispatch(Call & cx, const pa_hip_shape * s, const void * const * k_page
         return attn_decode(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
     // every other head-dim-128 call (verify, prefill, f16 K/V, odd head counts, padded heads)
     if (s->hd == 128) return attn_mma(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
-    // head dim 256 with fp16 queries (the reference engines' f16(q*scale), or f16 K in PA_QMODE_GGML): matrix cores;
-    // ggml's q8_0 query rounding over quantized K at head dim 256 stays on the generic kernel
-    if (s->qmode == PA_QMODE_F16 || s->fmt == PA_FMT_F16) return attn_mma(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
-    return attn_generic(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
+    // head dim 256: matrix cores (fp16 queries, or ggml's q8_0 query rounding with exact block dots over quantized K)
+    return attn_mma(cx, s, k_pages, v_pages, nkeys, n_pages, Q, O, m, l, st);
 }
 
 // no keys at all: (0, -inf, 0) by the merge kernel over zero slots (nothing else is launched)

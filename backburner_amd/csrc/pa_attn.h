@@ -11,8 +11,6 @@ namespace pa_hip {
 
 constexpr int MAXP = 64;   // pages per attention launch (more are split over several launches into one slot array)
 
-enum { CFG_DECODE = 0, CFG_MID = 1 };   // head dim 256 (attn_kernel): 16 / 64 rows per workgroup
-
 struct AttnArgs {
     const uint8_t * kp[MAXP];       // page base (key 0, head 0) of K / V
     const uint8_t * vp[MAXP];
@@ -31,7 +29,7 @@ struct AttnArgs {
     float scale;                    // softmax scale (PA_QMODE_F16 folds it into Q)
     float s_mul;                    // factor from the dot to base-2 logits (scale * log2 e, or log2 e)
     const float * q;                // [nkv][rows][hd] fp32
-    float * po;                     // slots [nkv][qr][slots][hd] (decode, MMA) or [slot][nkv][qr][hd] (attn_kernel)
+    float * po;                     // slots [nkv][qr][slots][hd]
     float2 * pml;                   // the same without hd: (max in base-2 units, sum)
     float * O, * m, * l;            // final [nkv][rows][hd], [nkv][rows]
 };
@@ -46,7 +44,6 @@ struct MergeArgs {
     float * lse = nullptr;          // and lse = m + log l [nkv][rows] (0 and -inf where l = 0)
 };
 
-hipError_t launch_attention(int hd, int fmt, int cfg, const AttnArgs & a, uint32_t grid, hipStream_t st);
 hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st);
 hipError_t launch_decode(int fmt, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0 = nullptr,
                          hipEvent_t ev1 = nullptr);
@@ -71,7 +68,6 @@ hipError_t launch_normalise(int hd, const float * O, const float * m, const floa
                             float * lse, hipStream_t st);
 hipError_t launch_coattn(int hd, const uint16_t * Oh, const float * lse, const float * Oloc, const float * mloc,
                          const float * lloc, uint64_t rows, float * out, float * lse_out, hipStream_t st);
-void cfg_geometry(int cfg, int & rows_per_wg, int & nb);
 
 #ifndef PA_ACCEPT_SEG
 #define PA_ACCEPT_SEG 16384

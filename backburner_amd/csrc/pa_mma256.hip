@@ -1,7 +1,10 @@
 // pa_mma256.hip - partial attention at head dim 256, the reference's compile-time shape (phone-attn.h:78-79: 48 query
 // rows = 8 tokens x GQA 6 per KV head), over q8_0 / q4_0 / f16 K and V on fp16 matrix cores (gfx950). Queries are
 // f16(q*scale) (PA_QMODE_F16, the reference engines' Qs, phone-attn.h:595-599), or f16(q) for f16 K in
-// PA_QMODE_GGML (ggml's f16 vec_dot type; the scale then multiplies the score).
+// PA_QMODE_GGML (ggml's f16 vec_dot type; the scale then multiplies the score). In PA_QMODE_GGML over quantized K
+// (EX) the scores are ggml's exact integer block dots: K staged as its integer quants with the block scales beside the
+// tile, Q as ggml's q8_0 quants times 2^-s_b; per 32-dim block one MFMA gives the integer dot and one more the
+// product of the key's and the row's block scales (see mm_prep_q in pa_mma.hip for the scale pair), summed in fp32.
 //
 // One workgroup = one KV head x one block of 64 query rows x one chunk of consecutive 32-key tiles; 4 waves of 16 rows
 // (48 rows: three waves compute, the fourth only stages). Per tile the workgroup dequantizes K and V once into LDS as
@@ -31,7 +34,8 @@ constexpr int M2_KST = 2 * M2_HD + 16;            // K row stride 528 B = 132 dw
 constexpr int M2_VST = 2 * M2_HD + 64;            // V row stride 576 B = 144 dwords: a transposing read's 4 rows x
                                                   // 32 bytes hit distinct banks
 constexpr int M2_KT = 32 * M2_KST, M2_VT = 32 * M2_VST;
-constexpr int M2_STAGE = M2_KT + M2_VT;           // 35,328 B per stage, two stages
+constexpr int M2_KSC = 32 * 16;                   // EX: the tile's K block scales, [key][8 blocks] fp16
+constexpr int M2_STAGE = M2_KT + M2_VT + M2_KSC;  // 35,840 B per stage, two stages
 
 // v_permlane16_swap of a value with itself gives every lane the values of lanes l & ~16 and l | 16
 __device__ __forceinline__ float m2_max16(float v) {    // max over lanes l and l ^ 16
@@ -44,8 +48,10 @@ __device__ __forceinline__ float m2_sum16(float v) {    // sum over lanes l and 
 }
 
 // SKIP: waves whose 16 rows are all past the call's rows only stage (one row block narrower than 64 rows).
-template <int FMT, bool SKIP>
+// EX: exact block dots in ggml's query rounding (quantized K only).
+template <int FMT, bool SKIP, bool EX>
 __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   // 2 waves per SIMD
+    static_assert(!EX || FMT != 0, "exact block dots need quantized K");
     // NB tiles' raw bytes are in flight while a tile is computed (a ring of NB register buffers); 3 to 5 measured no
     // faster than 2 at 48 rows x 4 KV heads x 65k q8_0 keys
     constexpr int NT = 256, NB = 2;
@@ -97,7 +103,12 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
             const int u = tid + NT * i;
             const int tensor = i >> 1, key = (u >> 4) & 31, blk = (u >> 1) & 7, half = u & 1;
             pa_u4 lo, hi;
-            mm_dequant<FMT>(Rb[i], half, lo, hi);
+            if (EX && tensor == 0) {                                 // K: integer quants, the block scale beside the tile
+                mm_dequant<FMT, true>(Rb[i], half, lo, hi);
+                if (half == 0) *(uint16_t *) (st + M2_KT + M2_VT + 16 * key + 2 * blk) = (uint16_t) Rb[i].d;
+            } else {
+                mm_dequant<FMT>(Rb[i], half, lo, hi);
+            }
             char * dst = (tensor ? st + M2_KT + key * M2_VST : st + key * M2_KST) + 2 * (32 * blk + 16 * half);
             *(pa_u4 *) dst = lo;
             *(pa_u4 *) (dst + 16) = hi;
@@ -110,9 +121,14 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- Q' as the B operand: lane (g, n) holds row n, dims 32 s + 8 g .. +7
+    // ---- Q' as the B operand: lane (g, n) holds row n, dims 32 s + 8 g .. +7. EX: per 32-dim block s, ggml's q8_0 quants
+    // (quantize_row_q8_0_ref: d = amax / 127, q = roundf(x / d); the block's 32 values sit in lanes n, n + 16, n + 32,
+    // n + 48) times 2^-s_b, exact in fp16, and in dqw[s] (lanes g = 0) the pair (hi, lo) summing to fp16(d) * scale *
+    // log2 e * 2^s_b to about 22 bits, s_b putting it in [8, 16)
     mm_h8 Qf[8];
+    uint32_t dqw[8];
     {
+        #pragma clang fp contract(off)
         const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * M2_HD + 8 * g;
         const uint32_t qmask = rlive ? 0xffffffffu : 0u;
         const float qs = a.qmode == 0 ? 1.0f : a.scale;
@@ -121,10 +137,29 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
             const pa_f4 x0 = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 32 * s)) & qmask);
             const pa_f4 x1 = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 32 * s + 4)) & qmask);
             mm_h8 f;
-            #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                f[t] = (_Float16) pa_f32(x0[t] * qs);                // f2h(q * scale)
-                f[t + 4] = (_Float16) pa_f32(x1[t] * qs);
+            if constexpr (EX) {
+                float am = fmaxf(fmaxf(fmaxf(fabsf(x0[0]), fabsf(x0[1])), fmaxf(fabsf(x0[2]), fabsf(x0[3]))),
+                                 fmaxf(fmaxf(fabsf(x1[0]), fabsf(x1[1])), fmaxf(fabsf(x1[2]), fabsf(x1[3]))));
+                am = mm_max32(m2_max16(am));
+                const float d = am / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                const float dq = (float) (_Float16) d * (a.scale * MM_LOG2E);
+                const int sb = dq > 0.0f ? min(14, 3 - __builtin_amdgcn_frexp_expf(dq) + 1) : 0;
+                const float v = __builtin_amdgcn_ldexpf(dq, sb);
+                const _Float16 hi = (_Float16) v, lo = (_Float16) (v - (float) hi);
+                dqw[s] = g == 0 ? (uint32_t) __builtin_bit_cast(uint16_t, hi) | ((uint32_t) __builtin_bit_cast(uint16_t, lo) << 16) : 0u;
+                #pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    f[t] = (_Float16) __builtin_amdgcn_ldexpf(roundf(x0[t] * id), -sb);
+                    f[t + 4] = (_Float16) __builtin_amdgcn_ldexpf(roundf(x1[t] * id), -sb);
+                }
+            } else {
+                dqw[s] = 0u;
+                #pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    f[t] = (_Float16) pa_f32(x0[t] * qs);            // f2h(q * scale)
+                    f[t + 4] = (_Float16) pa_f32(x1[t] * qs);
+                }
             }
             Qf[s] = f;
         }
@@ -138,7 +173,8 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
     #pragma unroll
     for (int db = 0; db < 16; db++) O[db] = (pa_f4){};
     float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
-    const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit
+    const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit (!EX)
+    float mc = 0.0f;                                                 // EX: the scores' offset, mref once finite (0 before)
     const mm_h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
 
     auto compute = [&](int stage, int nvalid) {
@@ -147,18 +183,49 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
         __builtin_amdgcn_s_waitcnt(0xc07f);                          // lgkmcnt(0): the stores and any scalar load done
         // ---- S^T = K Q'^T: the two key halves' chains interleaved, K read four steps ahead
         pa_f4 S[2] = {(pa_f4){}, (pa_f4){}};
-        mm_h8 kf[2][4];
+        constexpr int KA = EX ? 1 : 4;                               // K read KA steps ahead (EX holds more registers)
+        mm_h8 kf[2][KA];
         auto k_read = [&](int s) {
             #pragma unroll
-            for (int kh = 0; kh < 2; kh++) kf[kh][s & 3] = *(const mm_h8 *) (Kt + (16 * kh + n) * M2_KST + 2 * (32 * s + 8 * g));
+            for (int kh = 0; kh < 2; kh++) kf[kh][s % KA] = *(const mm_h8 *) (Kt + (16 * kh + n) * M2_KST + 2 * (32 * s + 8 * g));
         };
         #pragma unroll
-        for (int s = 0; s < 4; s++) k_read(s);
-        #pragma unroll
-        for (int s = 0; s < 8; s++) {
+        for (int s = 0; s < KA; s++) k_read(s);
+        if constexpr (EX) {
+            // per block s and key half kh: the integer dot times 2^-s_b, the scale product dk_s(key) * (hi + lo)(row)
+            // (dk_s at k = 0 and 1 of A in lanes g = 0, the row's pair at k = 0 and 1 of B), their product summed in
+            // block order from -mc: the base-2 logit minus the reference max
+            const uint32_t gmask = g == 0 ? 0xffffffffu : 0u;
+            uint32_t dk2[2];                                         // key 16 kh + n's fp16 scales of blocks s, s + 1
             #pragma unroll
-            for (int kh = 0; kh < 2; kh++) S[kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kh][s & 3], Qf[s], S[kh], 0, 0, 0);
-            if (s + 4 < 8) k_read(s + 4);
+            for (int s = 0; s < 8; s++) {
+                if ((s & 1) == 0) {
+                    #pragma unroll
+                    for (int kh = 0; kh < 2; kh++) dk2[kh] = *(const uint32_t *) (Kt + M2_KT + M2_VT + 16 * (16 * kh + n) + 2 * s);
+                }
+                #pragma unroll
+                for (int kh = 0; kh < 2; kh++) {
+                    const pa_f4 Sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kh][s % KA], Qf[s], (pa_f4){}, 0, 0, 0);
+                    const uint32_t dkw = pa_perm(0u, dk2[kh], (s & 1) ? 0x03020302u : 0x01000100u) & gmask;
+                    uint32_t dq = dqw[s];
+                    asm volatile("" : "+v"(dq));                     // the operand tuple built here, not held across
+                                                                     // tiles (8 tuples of 4 registers would spill)
+                    const pa_f4 Pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mm_h8, (pa_u4){dkw, 0u, 0u, 0u}),
+                                                                            __builtin_bit_cast(mm_h8, (pa_u4){dq, 0u, 0u, 0u}),
+                                                                            (pa_f4){}, 0, 0, 0);
+                    #pragma unroll
+                    for (int i = 0; i < 4; i++) S[kh][i] = fmaf(Pb[i], Sb[i], s == 0 ? -mc : S[kh][i]);
+                }
+                if (s + KA < 8) k_read(s + KA);
+                __builtin_amdgcn_sched_barrier(0);                   // one block at a time (registers)
+            }
+        } else {
+            #pragma unroll
+            for (int s = 0; s < 8; s++) {
+                #pragma unroll
+                for (int kh = 0; kh < 2; kh++) S[kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kh][s % KA], Qf[s], S[kh], 0, 0, 0);
+                if (s + KA < 8) k_read(s + KA);
+            }
         }
         if (nvalid < 32) {                                           // keys 16 kh + 4 g + i past the page's end
             #pragma unroll
@@ -168,7 +235,7 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
                     if (16 * kh + 4 * g + i >= nvalid) S[kh][i] = -INFINITY;
         }
         float tm = fmaxf(fmaxf(fmaxf(S[0][0], S[0][1]), fmaxf(S[0][2], S[0][3])), fmaxf(fmaxf(S[1][0], S[1][1]), fmaxf(S[1][2], S[1][3])));
-        tm = mm_max32(m2_max16(tm)) * sm;                            // row n's tile max, base 2
+        tm = EX ? mm_max32(m2_max16(tm)) + mc : mm_max32(m2_max16(tm)) * sm;   // row n's tile max, base 2
         if (__builtin_amdgcn_ballot_w64(tm > mref + MM_PMAX)) {
             const float mn = fmaxf(mref, tm);
             const float alpha = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mn);
@@ -176,13 +243,22 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
             for (int db = 0; db < 16; db++) O[db] *= alpha;
             lsum *= alpha;
             mref = mn;
+            if constexpr (EX) {                                      // rebase this tile's scores to the new offset
+                const float dl = mn - mc;
+                #pragma unroll
+                for (int kh = 0; kh < 2; kh++)
+                    #pragma unroll
+                    for (int i = 0; i < 4; i++) S[kh][i] -= dl;
+                mc = mn;
+            }
         }
         mx = fmaxf(mx, tm);
         mm_h8 P;
         #pragma unroll
         for (int kh = 0; kh < 2; kh++)
             #pragma unroll
-            for (int i = 0; i < 4; i++) P[4 * kh + i] = (_Float16) __builtin_amdgcn_exp2f(fmaf(S[kh][i], sm, -mref));
+            for (int i = 0; i < 4; i++)
+                P[4 * kh + i] = (_Float16) __builtin_amdgcn_exp2f(EX ? S[kh][i] : fmaf(S[kh][i], sm, -mref));
         #pragma unroll
         for (int t = 0; t < 8; t += 2) {                             // the row sum of the fp16 P the PV MFMAs use
             const mm_h2 pp = {P[t], P[t + 1]};
@@ -239,14 +315,20 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
     }
 }
 
+// ggml's query rounding over quantized K takes the exact block dots; f16 queries (and f16 K) the fp16 operands
 hipError_t launch_mma256(int fmt, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    switch (fmt * 2 + (skip ? 1 : 0)) {
-        case 0: hipExtLaunchKernelGGL((mma256_kernel<0, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 1: hipExtLaunchKernelGGL((mma256_kernel<0, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 2: hipExtLaunchKernelGGL((mma256_kernel<1, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 3: hipExtLaunchKernelGGL((mma256_kernel<1, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 4: hipExtLaunchKernelGGL((mma256_kernel<2, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 5: hipExtLaunchKernelGGL((mma256_kernel<2, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+    const bool ex = a.qmode == 0 && fmt != 0;
+    switch (fmt * 4 + (skip ? 2 : 0) + (ex ? 1 : 0)) {
+        case 0: hipExtLaunchKernelGGL((mma256_kernel<0, false, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 2: hipExtLaunchKernelGGL((mma256_kernel<0, true, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 4: hipExtLaunchKernelGGL((mma256_kernel<1, false, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 5: hipExtLaunchKernelGGL((mma256_kernel<1, false, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 6: hipExtLaunchKernelGGL((mma256_kernel<1, true, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 7: hipExtLaunchKernelGGL((mma256_kernel<1, true, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 8: hipExtLaunchKernelGGL((mma256_kernel<2, false, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 9: hipExtLaunchKernelGGL((mma256_kernel<2, false, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 10: hipExtLaunchKernelGGL((mma256_kernel<2, true, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 11: hipExtLaunchKernelGGL((mma256_kernel<2, true, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -429,7 +429,7 @@ def main():
     if args.secondary:
         l2, r2, _, _ = run_config(bb, ws, bb.FMT_Q8_0, 16, 65536, 48, max(2, min(args.steps, 10)), 1,
                                   "48 rows x 4 KV heads, head dim 256, 65536 q8_0 keys, 16 layers, ggml's q8_0 query "
-                                  "rounding (the generic head-dim-256 kernel)", nkv=4, hd=256)
+                                  "rounding (the head-dim-256 kernel with exact block dots)", nkv=4, hd=256)
         l2.close()
         log("secondary", json.dumps(r2))
         secondary.append(r2)

@@ -181,8 +181,8 @@ def test_mma_split_invariance(ws, fmt, rows):
                                                (bb.FMT_Q8_0, 48, 256, bb.QMODE_F16), (bb.FMT_Q8_0, 48, 256, bb.QMODE_GGML)])
 @pytest.mark.parametrize("chunk", [64, 1000, 4096])
 def test_chunk_keys(ws, fmt, rows, hd, qmode, chunk):
-    """config_req.gpu_chunk (keys per workgroup, pa_hip_ws_set_chunk_keys) on the decode, verify, head-dim-256 matrix-core
-    and head-dim-256 generic kernels: every chunking within the parity bar of the oracle."""
+    """config_req.gpu_chunk (keys per workgroup, pa_hip_ws_set_chunk_keys) on the decode, verify and head-dim-256 kernels
+    (fp16 queries, and ggml's rounding with exact block dots): every chunking within the parity bar of the oracle."""
     nkv, nk = 2, 5000
     print(f"chunk keys {chunk}: fmt={fmt} rows={rows} hd={hd} qmode={qmode}", flush=True)
     K, V, Q, rs = case(fmt, nkv, rows, hd, nk, 1200 + chunk + rows)

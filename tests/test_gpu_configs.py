@@ -11,7 +11,7 @@ O, m and l; orc_attn_ggml in PA_QMODE_GGML):
 - more than 256 split-K slots (a decode over 65 pages: two launches, 272 slots, the generic merge);
 - pages whose byte size exceeds 2^32 (rows of 4,352 bytes, 2^20 + 100 keys), through the decode and the matrix-core
   kernels;
-- head dim 256 calls small enough for a single chunk (the generic kernel writes the result itself), and the
+- head dim 256 calls small enough for a single chunk (the kernel writes the result itself), and the
   reference's own shape (4 KV heads x 48 rows, head dim 256) at 65,536 keys on the head-dim-256 matrix-core kernel.
 
 Every test prints its errors; the margins are recorded in the design notes."""
@@ -188,7 +188,7 @@ def test_page_above_4_gib(ws, rows):
 
 @pytest.mark.parametrize("rows,qmode", [(8, bb.QMODE_GGML), (48, bb.QMODE_GGML), (48, bb.QMODE_F16)])
 def test_hd256_single_chunk(ws, rows, qmode):
-    """Head dim 256 over 40 keys (one chunk): the generic kernel writes (O, m, l) itself, no merge."""
+    """Head dim 256 over 40 keys (one chunk): the head-dim-256 kernel writes (O, m, l) itself, no merge."""
     print(f"hd 256 single chunk rows={rows} qmode={qmode}", flush=True)
     c = DevCase(bb.FMT_Q8_0, 2, rows, 40, 4601 + rows + qmode, hd=256)
     try:
