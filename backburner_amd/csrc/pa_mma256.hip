@@ -28,14 +28,16 @@
 
 namespace pa_hip {
 
-constexpr int M2_HD = 256;
-constexpr int M2_KST = 2 * M2_HD + 16;            // K row stride 528 B = 132 dwords: 16 keys' 16-byte reads at one dim
-                                                  // offset hit distinct banks
-constexpr int M2_VST = 2 * M2_HD + 64;            // V row stride 576 B = 144 dwords: a transposing read's 4 rows x
-                                                  // 32 bytes hit distinct banks
-constexpr int M2_KT = 32 * M2_KST, M2_VT = 32 * M2_VST;
-constexpr int M2_KSC = 32 * 16;                   // EX: the tile's K block scales, [key][8 blocks] fp16
-constexpr int M2_STAGE = M2_KT + M2_VT + M2_KSC;  // 35,840 B per stage, two stages
+// LDS geometry per head dim: K row stride 2 HD + 16 B (528 B = 132 dwords at 256, 272 B = 68 at 128: 16 keys' 16-byte
+// reads at one dim offset hit distinct banks), V row stride 2 HD + 64 B (576 / 320 B: a transposing read's 4 rows x
+// 32 bytes hit distinct banks), and for EX the tile's K block scales [key][HD / 32 blocks] fp16. Two stages: 35,840 B
+// each at head dim 256, 19,200 B at 128.
+template <int HD> struct M2Geom {
+    static constexpr int NBLK = HD / 32;                      // quant blocks per head row
+    static constexpr int KST = 2 * HD + 16, VST = 2 * HD + 64;
+    static constexpr int KT = 32 * KST, VT = 32 * VST, KSC = 32 * 2 * NBLK;
+    static constexpr int STAGE = KT + VT + KSC;
+};
 
 // v_permlane16_swap of a value with itself gives every lane the values of lanes l & ~16 and l | 16
 __device__ __forceinline__ float m2_max16(float v) {    // max over lanes l and l ^ 16
@@ -48,14 +50,19 @@ __device__ __forceinline__ float m2_sum16(float v) {    // sum over lanes l and 
 }
 
 // SKIP: waves whose 16 rows are all past the call's rows only stage (one row block narrower than 64 rows).
-// EX: exact block dots in ggml's query rounding (quantized K only).
-template <int FMT, bool SKIP, bool EX>
-__global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   // 2 waves per SIMD
+// EX: exact block dots in ggml's query rounding (quantized K only). WPS: waves per SIMD the registers are sized for.
+// Instantiated at head dim 256; at 128 (three waves per SIMD, 167 VGPRs) the 16-row waves measured slower than the
+// 32-row mma_kernel on verify (157 against 111 us), each wave reading the whole K / V^T tile from LDS.
+template <int HD, int FMT, bool SKIP, bool EX, int WPS>
+__global__ __launch_bounds__(256, WPS) void mma256_kernel(const AttnArgs a) {
     static_assert(!EX || FMT != 0, "exact block dots need quantized K");
+    using G2 = M2Geom<HD>;
+    constexpr int NBLK = G2::NBLK, M2_KST = G2::KST, M2_VST = G2::VST, M2_KT = G2::KT, M2_VT = G2::VT;
+    constexpr int M2_STAGE = G2::STAGE;
     // NB tiles' raw bytes are in flight while a tile is computed (a ring of NB register buffers); 3 to 5 measured no
     // faster than 2 at 48 rows x 4 KV heads x 65k q8_0 keys
     constexpr int NT = 256, NB = 2;
-    constexpr int UPT = 1024 / NT;                                   // staging units per thread (1024 per tile)
+    constexpr int UPT = 128 * NBLK / NT;                             // staging units per thread (128 NBLK per tile)
     __shared__ __attribute__((aligned(16))) char smem[2 * M2_STAGE];
 
     // ---- which (chunk, KV head, row block): row blocks fastest, consecutive items on one XCD (blockIdx % 8 in dispatch
@@ -78,7 +85,8 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
     MmCursor cl, cc;
     cl.init(a); cc.init(a);
 
-    // ---- staging units: u = tid + 256 i -> tensor i >> 1 (uniform), key (u >> 4) & 31, block (u >> 1) & 7, half u & 1
+    // ---- staging units: u = tid + 256 i -> tensor 4 i / NBLK (uniform), key (u / (2 NBLK)) & 31, block (u >> 1) &
+    // (NBLK - 1), half u & 1
     using F = MmFmt<FMT>;
     MmRaw<FMT> R[NB][UPT];                                           // tile j's raw bytes in R[j % NB]
     auto load_tile = [&](MmRaw<FMT> (&Rb)[UPT], uint32_t tau, bool live) {
@@ -89,7 +97,7 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
         #pragma unroll
         for (int i = 0; i < UPT; i++) {
             const int u = tid + NT * i;
-            const int tensor = i >> 1, key = (u >> 4) & 31, blk = (u >> 1) & 7, half = u & 1;
+            const int tensor = 4 * i / NBLK, key = (u / (2 * NBLK)) & 31, blk = (u >> 1) & (NBLK - 1), half = u & 1;
             const uint8_t * base = (tensor ? cl.vb : cl.kb) + (size_t) h * a.hb + (size_t) j0 * a.rs;
             const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *) base, (short) 0, (int) nrec, 0x00020000);
             mm_load_unit_buf_al<FMT>(Rb[i], rsrc, min((uint32_t) key, last) * a.rs + blk * F::BB, half,
@@ -101,11 +109,11 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
         #pragma unroll
         for (int i = 0; i < UPT; i++) {
             const int u = tid + NT * i;
-            const int tensor = i >> 1, key = (u >> 4) & 31, blk = (u >> 1) & 7, half = u & 1;
+            const int tensor = 4 * i / NBLK, key = (u / (2 * NBLK)) & 31, blk = (u >> 1) & (NBLK - 1), half = u & 1;
             pa_u4 lo, hi;
             if (EX && tensor == 0) {                                 // K: integer quants, the block scale beside the tile
                 mm_dequant<FMT, true>(Rb[i], half, lo, hi);
-                if (half == 0) *(uint16_t *) (st + M2_KT + M2_VT + 16 * key + 2 * blk) = (uint16_t) Rb[i].d;
+                if (half == 0) *(uint16_t *) (st + M2_KT + M2_VT + 2 * NBLK * key + 2 * blk) = (uint16_t) Rb[i].d;
             } else {
                 mm_dequant<FMT>(Rb[i], half, lo, hi);
             }
@@ -125,15 +133,15 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
     // (quantize_row_q8_0_ref: d = amax / 127, q = roundf(x / d); the block's 32 values sit in lanes n, n + 16, n + 32,
     // n + 48) times 2^-s_b, exact in fp16, and in dqw[s] (lanes g = 0) the pair (hi, lo) summing to fp16(d) * scale *
     // log2 e * 2^s_b to about 22 bits, s_b putting it in [8, 16)
-    mm_h8 Qf[8];
-    uint32_t dqw[8];
+    mm_h8 Qf[NBLK];
+    uint32_t dqw[NBLK];
     {
         #pragma clang fp contract(off)
-        const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * M2_HD + 8 * g;
+        const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * HD + 8 * g;
         const uint32_t qmask = rlive ? 0xffffffffu : 0u;
         const float qs = a.qmode == 0 ? 1.0f : a.scale;
         #pragma unroll
-        for (int s = 0; s < 8; s++) {
+        for (int s = 0; s < NBLK; s++) {
             const pa_f4 x0 = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 32 * s)) & qmask);
             const pa_f4 x1 = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 32 * s + 4)) & qmask);
             mm_h8 f;
@@ -169,9 +177,9 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
     load_tile(R[0], t0 + NB, ntiles > NB);
     mm_lds_barrier();
 
-    pa_f4 O[16];
+    pa_f4 O[HD / 16];
     #pragma unroll
-    for (int db = 0; db < 16; db++) O[db] = (pa_f4){};
+    for (int db = 0; db < HD / 16; db++) O[db] = (pa_f4){};
     float mref = -INFINITY, mx = -INFINITY, lsum = 0.0f;
     const float sm = a.qmode == 0 && FMT == 0 ? a.scale * MM_LOG2E : MM_LOG2E;   // score -> base-2 logit (!EX)
     float mc = 0.0f;                                                 // EX: the scores' offset, mref once finite (0 before)
@@ -183,7 +191,7 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
         __builtin_amdgcn_s_waitcnt(0xc07f);                          // lgkmcnt(0): the stores and any scalar load done
         // ---- S^T = K Q'^T: the two key halves' chains interleaved, K read four steps ahead
         pa_f4 S[2] = {(pa_f4){}, (pa_f4){}};
-        constexpr int KA = EX ? 1 : 4;                               // K read KA steps ahead (EX holds more registers)
+        constexpr int KA = EX ? 1 : (NBLK < 4 ? NBLK : 4);           // K read KA steps ahead (EX holds more registers)
         mm_h8 kf[2][KA];
         auto k_read = [&](int s) {
             #pragma unroll
@@ -198,10 +206,11 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
             const uint32_t gmask = g == 0 ? 0xffffffffu : 0u;
             uint32_t dk2[2];                                         // key 16 kh + n's fp16 scales of blocks s, s + 1
             #pragma unroll
-            for (int s = 0; s < 8; s++) {
+            for (int s = 0; s < NBLK; s++) {
                 if ((s & 1) == 0) {
                     #pragma unroll
-                    for (int kh = 0; kh < 2; kh++) dk2[kh] = *(const uint32_t *) (Kt + M2_KT + M2_VT + 16 * (16 * kh + n) + 2 * s);
+                    for (int kh = 0; kh < 2; kh++)
+                        dk2[kh] = *(const uint32_t *) (Kt + M2_KT + M2_VT + 2 * NBLK * (16 * kh + n) + 2 * s);
                 }
                 #pragma unroll
                 for (int kh = 0; kh < 2; kh++) {
@@ -216,15 +225,15 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
                     #pragma unroll
                     for (int i = 0; i < 4; i++) S[kh][i] = fmaf(Pb[i], Sb[i], s == 0 ? -mc : S[kh][i]);
                 }
-                if (s + KA < 8) k_read(s + KA);
+                if (s + KA < NBLK) k_read(s + KA);
                 __builtin_amdgcn_sched_barrier(0);                   // one block at a time (registers)
             }
         } else {
             #pragma unroll
-            for (int s = 0; s < 8; s++) {
+            for (int s = 0; s < NBLK; s++) {
                 #pragma unroll
                 for (int kh = 0; kh < 2; kh++) S[kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kh][s % KA], Qf[s], S[kh], 0, 0, 0);
-                if (s + KA < 8) k_read(s + KA);
+                if (s + KA < NBLK) k_read(s + KA);
             }
         }
         if (nvalid < 32) {                                           // keys 16 kh + 4 g + i past the page's end
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
             const float mn = fmaxf(mref, tm);
             const float alpha = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mn);
             #pragma unroll
-            for (int db = 0; db < 16; db++) O[db] *= alpha;
+            for (int db = 0; db < HD / 16; db++) O[db] *= alpha;
             lsum *= alpha;
             mref = mn;
             if constexpr (EX) {                                      // rebase this tile's scores to the new offset
@@ -268,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
         // dims 16 db + 4 (L % 4) .. +3; lane (g, s) then holds dim 16 db + s of keys 16 r + 4 g + j (j < 4)
         const char * vrow = Vt + (4 * g + (n >> 2)) * M2_VST + 2 * 4 * (n & 3);
         #pragma unroll
-        for (int db = 0; db < 16; db++) {
+        for (int db = 0; db < HD / 16; db++) {
             const pa_h4 x0 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vrow + 32 * db)));
             const pa_h4 x1 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vrow + 16 * M2_VST + 32 * db)));
             const mm_h8 va = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -301,10 +310,10 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
     const float f = mref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref - mx);
     if (!rlive) return;
     const bool direct = a.n_chunks == 1 && a.fused;
-    float * dst = direct ? a.O + ((size_t) h * a.rows + row) * M2_HD
-                         : a.po + (((size_t) h * a.qr + row) * a.slots + a.slot0 + c) * M2_HD;
+    float * dst = direct ? a.O + ((size_t) h * a.rows + row) * HD
+                         : a.po + (((size_t) h * a.qr + row) * a.slots + a.slot0 + c) * HD;
     #pragma unroll
-    for (int db = 0; db < 16; db++) *(pa_f4 *) (dst + 16 * db + 4 * g) = O[db] * f;
+    for (int db = 0; db < HD / 16; db++) *(pa_f4 *) (dst + 16 * db + 4 * g) = O[db] * f;
     if (g == 0) {
         if (direct) {
             a.m[(size_t) h * a.rows + row] = mx == -INFINITY ? -INFINITY : mx * PA_LN2;
@@ -315,23 +324,28 @@ __global__ __launch_bounds__(256, 2) void mma256_kernel(const AttnArgs a) {   //
     }
 }
 
-// ggml's query rounding over quantized K takes the exact block dots; f16 queries (and f16 K) the fp16 operands
-hipError_t launch_mma256(int fmt, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    const bool ex = a.qmode == 0 && fmt != 0;
+template <int HD, int WPS>
+static hipError_t launch_m16(int fmt, bool skip, bool ex, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0,
+                             hipEvent_t ev1) {
     switch (fmt * 4 + (skip ? 2 : 0) + (ex ? 1 : 0)) {
-        case 0: hipExtLaunchKernelGGL((mma256_kernel<0, false, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 2: hipExtLaunchKernelGGL((mma256_kernel<0, true, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 4: hipExtLaunchKernelGGL((mma256_kernel<1, false, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 5: hipExtLaunchKernelGGL((mma256_kernel<1, false, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 6: hipExtLaunchKernelGGL((mma256_kernel<1, true, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 7: hipExtLaunchKernelGGL((mma256_kernel<1, true, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 8: hipExtLaunchKernelGGL((mma256_kernel<2, false, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 9: hipExtLaunchKernelGGL((mma256_kernel<2, false, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 10: hipExtLaunchKernelGGL((mma256_kernel<2, true, false>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
-        case 11: hipExtLaunchKernelGGL((mma256_kernel<2, true, true>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 0: hipExtLaunchKernelGGL((mma256_kernel<HD, 0, false, false, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 2: hipExtLaunchKernelGGL((mma256_kernel<HD, 0, true, false, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 4: hipExtLaunchKernelGGL((mma256_kernel<HD, 1, false, false, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 5: hipExtLaunchKernelGGL((mma256_kernel<HD, 1, false, true, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 6: hipExtLaunchKernelGGL((mma256_kernel<HD, 1, true, false, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 7: hipExtLaunchKernelGGL((mma256_kernel<HD, 1, true, true, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 8: hipExtLaunchKernelGGL((mma256_kernel<HD, 2, false, false, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 9: hipExtLaunchKernelGGL((mma256_kernel<HD, 2, false, true, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 10: hipExtLaunchKernelGGL((mma256_kernel<HD, 2, true, false, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
+        case 11: hipExtLaunchKernelGGL((mma256_kernel<HD, 2, true, true, WPS>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+// ggml's query rounding over quantized K takes the exact block dots; f16 queries (and f16 K) the fp16 operands
+hipError_t launch_mma256(int fmt, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    return launch_m16<256, 2>(fmt, skip, a.qmode == 0 && fmt != 0, a, grid, st, ev0, ev1);
 }
 
 }  // namespace pa_hip
