@@ -418,7 +418,7 @@ def main():
         extra["reference_shape"] = workload(
             bb, ws, args, "reference_shape", bb.FMT_Q8_0, nl, 65536, 48,
             f"the reference's own shape: 8 tokens x GQA 6 = 48 rows x 4 KV heads, head dim 256, queries f16(q*scale) "
-            f"(scale 1/16), 65536 q8_0 keys, {nl} layers", "hbm", "pa_hip::mma256_kernel<1, true> (q8_0, head dim 256)",
+            f"(scale 1/16), 65536 q8_0 keys, {nl} layers", "hbm", "pa_hip::mma256_kernel<256, 1, true, false, 2> (q8_0, head dim 256)",
             max(2, min(args.steps, 10)), 0, outliers=0, pmc="reference_shape", nkv=4, hd=256, qmode=bb.QMODE_F16,
             scale=1.0 / 16)
     if want("accept"):
