@@ -188,16 +188,17 @@ private:
                int ng) {
         const call_geom g = geom_of(cfg, ng, ntok_hint);
         nkv_ = g.nkv; ng_ = g.ng; nt_ = g.nt; last_rows_ = g.rows;
+        if (!ensure(g.dev_bytes(), g.host_bytes())) return false;   // (a growth drops the armed graph: it names the buffers)
         const bool hit = armed_match(pages, nkeys, n_pages, cfg, ng, g.nt);
-        if (!hit) disarm();
-        if (!ensure(g.dev_bytes(), g.host_bytes())) return false;
+        if (!hit) disarm();                                          // the stream is idle: the previous call has ended
         if (!upload_rows(pages, nkeys, n_pages, cfg.rs)) return false;
         std::memcpy(hbuf_, Qs, g.srows * pa::HD * 2);
         hout_ = (const float *) (hbuf_ + g.qs_b);
         if (hit) {                                                   // the armed launch sequence, timed as a whole
             const bool ok = hipEventRecord(e0_, st_) == hipSuccess && hipGraphLaunch(armed_.exec, st_) == hipSuccess &&
                             hipEventRecord(e1_, st_) == hipSuccess;
-            disarm();
+            armed_.used = true;                                      // one call per arm; destroyed once the stream is
+                                                                     // idle (the next arm / call / page free)
             if (!ok) return fail("armed graph launch");
             n_armed_hits_++;
             return true;
@@ -233,7 +234,7 @@ private:
     // the armed graph is for exactly these pages, key counts, tokens and row format, one group
     bool armed_match(const pa::page * pages, const uint32_t * nkeys, int n_pages, const pa::config_req & cfg, int ng,
                      uint32_t nt) const {
-        if (!armed_.exec || ng != 1 || (int) armed_.hk.size() != n_pages || armed_.nt != nt || armed_.rs != cfg.rs ||
+        if (!armed_.exec || armed_.used || ng != 1 || (int) armed_.hk.size() != n_pages || armed_.nt != nt || armed_.rs != cfg.rs ||
             armed_.hb != cfg.hb || armed_.is_q8 != cfg.is_q8 || armed_.nkv != cfg.n_head_kv || armed_.chunk != cfg.gpu_chunk)
             return false;
         for (int i = 0; i < n_pages; i++) if (armed_.hk[i] != pages[i].hk || armed_.nkeys[i] != nkeys[i]) return false;
@@ -350,6 +351,7 @@ private:
         std::vector<void *> hk;
         std::vector<uint32_t> nkeys;
         uint32_t rs = 0, hb = 0, is_q8 = 0, nkv = 0, chunk = 0, nt = 0;
+        bool used = false;                    // launched by a call: kept until the stream is idle, never matched again
     } armed_;
     uint64_t n_armed_ = 0, n_armed_hits_ = 0, n_warm_ = 0;
     std::mutex gate_mu_;                      // close(): no call in flight, none started after it
