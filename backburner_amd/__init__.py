@@ -146,6 +146,10 @@ def synth() -> C.CDLL:
     L.pa_synth_malloc.argtypes = [C.c_size_t]
     L.pa_synth_free.restype = C.c_int
     L.pa_synth_free.argtypes = [vp]
+    L.pa_synth_host_alloc.restype = vp
+    L.pa_synth_host_alloc.argtypes = [C.c_size_t]
+    L.pa_synth_host_free.restype = C.c_int
+    L.pa_synth_host_free.argtypes = [vp]
     L.pa_synth_memset.restype = C.c_int
     L.pa_synth_memset.argtypes = [vp, C.c_int, C.c_size_t]
     L.pa_synth_h2d.restype = C.c_int
@@ -232,6 +236,24 @@ class DeviceBuffer:
             self.close()
         except Exception:
             pass
+
+
+class PinnedArray:
+    """A numpy array over pinned host memory (hipHostMalloc), as the HIP server engine's pages are; freed on close()."""
+
+    def __init__(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        self.ptr = synth().pa_synth_host_alloc(max(a.nbytes, 1))
+        if not self.ptr:
+            raise PaHipError(f"hipHostMalloc({a.nbytes}) failed")
+        self.array = np.ctypeslib.as_array((C.c_uint8 * a.nbytes).from_address(self.ptr)).view(a.dtype).reshape(a.shape)
+        self.array[...] = a
+
+    def close(self) -> None:
+        if getattr(self, "ptr", None):
+            self.array = None
+            synth().pa_synth_host_free(self.ptr)
+            self.ptr = None
 
 
 def device_sync() -> None:

@@ -683,10 +683,13 @@ void compat_shape(int & nr, int & hd) {
     nr = g_nr.load(); hd = g_hd.load();
 }
 
-bool is_device_ptr(const void * p) {
+// where a caller's buffer lives: device memory (used in place), pinned host memory the runtime already owns
+// (hipHostMalloc: copied to the device directly), or pageable host memory (copied into pinned staging first)
+enum class Mem { device, pinned, pageable };
+Mem mem_kind(const void * p) {
     hipPointerAttribute_t at;
-    if (hipPointerGetAttributes(&at, p) != hipSuccess) { (void) hipGetLastError(); return false; }
-    return at.type == hipMemoryTypeDevice;
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) { (void) hipGetLastError(); return Mem::pageable; }
+    return at.type == hipMemoryTypeDevice ? Mem::device : at.type == hipMemoryTypeHost ? Mem::pinned : Mem::pageable;
 }
 
 void fail_out(float * O, float * m, float * l, size_t rows, int hd) {
@@ -723,11 +726,12 @@ bool ensure_pinned(pa_hip_ws * w, size_t need) {
 size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 
 // one synchronous call of the engine path for `nkv` heads at K/V (host or device), reference rounding (f16 Q*scale).
-// Host buffers are never handed to the HIP runtime: K/V spans and Q rows are copied into the workspace's pinned staging
-// on the calling thread, only pinned <-> device copies are enqueued, and the results come back through the same
-// staging. So concurrent calls from several threads (the server's sme_page, phone-attn.h:509-520) never make the
-// runtime pin or stage the callers' pageable pages, and a call's host buffers are not touched by a transfer after it
-// returns. The wait for the stream is bounded (wait_limit_ms).
+// Pageable host buffers are never handed to the HIP runtime: K/V spans and Q rows are copied into the workspace's
+// pinned staging on the calling thread, only pinned <-> device copies are enqueued, and the results come back through
+// the same staging. So concurrent calls from several threads (the server's sme_page, phone-attn.h:509-520) never make
+// the runtime pin or stage the callers' pageable pages, and a call's host buffers are not touched by a transfer after
+// it returns. K/V spans already in pinned memory (the HIP server engine's pages) are copied to the device directly.
+// The wait for the stream is bounded (wait_limit_ms).
 bool compat_call(pa_hip_ws * w, const float * Q, int qrs, int qhs, const uint8_t * K, const uint8_t * V, size_t rs, size_t hb,
                  int fmt, int nkv, int nk, float scale, float * O, float * m, float * l) {
     InFlight inflight;
@@ -749,23 +753,26 @@ bool compat_call(pa_hip_ws * w, const float * Q, int qrs, int qhs, const uint8_t
     const uint32_t hbmin = head_bytes(fmt, HD);
     // K/V: device pointers are used in place; host rows are staged (rows [0, nk) of every head in the span)
     const size_t span = (size_t) (nk - 1) * rs + (size_t) (nkv - 1) * hb + hbmin;
-    const bool k_host = !is_device_ptr(K), v_host = !is_device_ptr(V);
+    const Mem k_mem = mem_kind(K), v_mem = mem_kind(V);
+    const bool k_stage = k_mem == Mem::pageable, v_stage = v_mem == Mem::pageable;
     const size_t q_b = rows * HD * sizeof(float), o_b = rows * (HD + 2) * sizeof(float);
-    // pinned layout: [K span][V span][Q][O, m, l]
-    const size_t hk_off = 0, hv_off = k_host ? al256(span) : 0, hq_off = hv_off + (v_host ? al256(span) : 0);
+    // pinned layout: [K span][V span][Q][O, m, l] (the spans only for pageable sources)
+    const size_t hk_off = 0, hv_off = k_stage ? al256(span) : 0, hq_off = hv_off + (v_stage ? al256(span) : 0);
     const size_t ho_off = hq_off + al256(q_b);
     if (!ensure_pinned(w, ho_off + o_b)) return false;
     const uint8_t * dK = K, * dV = V;
-    if (k_host) {
+    if (k_mem != Mem::device) {
         if (!ensure(w, w->dk, w->dk_cap, span, st, false, "hipMalloc K staging")) return false;
-        std::memcpy(w->hst + hk_off, K, span);
-        if (!hip_ok(hipMemcpyAsync(w->dk, w->hst + hk_off, span, hipMemcpyHostToDevice, st), "K upload")) return false;
+        const void * src = K;
+        if (k_stage) { std::memcpy(w->hst + hk_off, K, span); src = w->hst + hk_off; }
+        if (!hip_ok(hipMemcpyAsync(w->dk, src, span, hipMemcpyHostToDevice, st), "K upload")) return false;
         dK = w->dk;
     }
-    if (v_host) {
+    if (v_mem != Mem::device) {
         if (!ensure(w, w->dv, w->dv_cap, span, st, false, "hipMalloc V staging")) return false;
-        std::memcpy(w->hst + hv_off, V, span);
-        if (!hip_ok(hipMemcpyAsync(w->dv, w->hst + hv_off, span, hipMemcpyHostToDevice, st), "V upload")) return false;
+        const void * src = V;
+        if (v_stage) { std::memcpy(w->hst + hv_off, V, span); src = w->hst + hv_off; }
+        if (!hip_ok(hipMemcpyAsync(w->dv, src, span, hipMemcpyHostToDevice, st), "V upload")) return false;
         dV = w->dv;
     }
     if (!ensure(w, w->dq, w->dq_cap, q_b, st, false, "hipMalloc Q staging") ||

@@ -130,6 +130,8 @@ int pa_synth_read(const void * src, int64_t bytes, int blocks, uint32_t * sink, 
 // ---- plumbing
 void * pa_synth_malloc(size_t bytes) { void * p = nullptr; return hipMalloc(&p, bytes) == hipSuccess ? p : nullptr; }
 int pa_synth_free(void * p) { return hipFree(p) == hipSuccess ? 0 : -1; }
+void * pa_synth_host_alloc(size_t bytes) { void * p = nullptr; return hipHostMalloc(&p, bytes, hipHostMallocDefault) == hipSuccess ? p : nullptr; }
+int pa_synth_host_free(void * p) { return hipHostFree(p) == hipSuccess ? 0 : -1; }
 int pa_synth_memset(void * p, int v, size_t bytes) { return hipMemset(p, v, bytes) == hipSuccess ? 0 : -1; }
 int pa_synth_h2d(void * dst, const void * src, size_t bytes) { return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1; }
 int pa_synth_d2h(void * dst, const void * src, size_t bytes) { return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1; }

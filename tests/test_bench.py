@@ -36,13 +36,14 @@ def test_committed_traffic_summary():
     assert "dec_kernel" in (ROOT / "profiles" / "bench_all_kernels.md").read_text()
 
 
-@pytest.mark.parametrize("name,kernel,flop", [("prefill", "mma_kernel<1, 8, true, false, false>", 4 * 4096 * 65536 * 128 * 8),
+@pytest.mark.parametrize("name,kernel,flop", [("prefill", "mma_kernel<1, 8, true, false, true>", 4 * 4096 * 65536 * 128 * 8),
+                                              ("prefill_f16", "mma_kernel<1, 8, false, false, false>", 4 * 4096 * 65536 * 128 * 8),
                                               ("verify", "mma_kernel<1, 4, true, false, true>", 4 * 128 * 98304 * 128 * 8),
-                                              ("reference_shape", "mma256_kernel<1, true>", 4 * 48 * 65536 * 256 * 4)])
+                                              ("reference_shape", "mma256_kernel<256, 1, true, false, 2>", 4 * 48 * 65536 * 256 * 4)])
 def test_committed_mma_counters(name, kernel, flop):
     """The matrix-core kernels' counter summaries: the fp16 MFMA work the counters saw (MOPS_F16 x 512) is the
-    algorithmic flops (verify adds its scale-product MFMAs), K/V are fetched about once, and the MFMA busy fraction is
-    derived from the raw cycle counters."""
+    algorithmic flops (the exact-dot forms add their scale-product MFMAs, at most 1.3x), K/V are fetched about once,
+    and the MFMA busy fraction is derived from the raw cycle counters."""
     d = json.loads((ROOT / "profiles" / f"{name}_pmc.json").read_text())
     c = d["counters"]
     assert kernel in d["kernel"] and d["flop_per_launch"] == flop

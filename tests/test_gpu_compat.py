@@ -88,6 +88,43 @@ def test_sme_attn_partial_concurrent_threads():
     assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
 
 
+def test_sme_attn_partial_pinned_pages():
+    """K/V in pinned host memory (hipHostMalloc, as the HIP server engine allocates its pages for the reference server,
+    whose CPU-engine path then hands them to sme_attn_partial): copied to the device directly, no staging copy. Eight
+    threads at once over one page, results bit-identical to the same calls over pageable copies of the bytes."""
+    import threading
+    nkv, nk = 8, 4096
+    K, V, Q, rs, hb = ref_case(bb.FMT_Q8_0, nkv, nk, 51)
+    pk, pv = bb.PinnedArray(K), bb.PinnedArray(V)
+    ws = [bb.sme_ws_new() for _ in range(nkv)]
+    try:
+        def run(Kx, Vx, threaded):
+            O = np.zeros((nkv * NR, HD), np.float32); m = np.zeros(nkv * NR, np.float32); l = np.zeros(nkv * NR, np.float32)
+            call = lambda h: bb.sme_attn_partial(ws[h], Q[h * NR:], HD, Kx, Vx, rs, 1, nk, 1.0 / 16, 512, O[h * NR:], m[h * NR:],
+                                                  l[h * NR:], k_off=h * hb)
+            if threaded:
+                th = [threading.Thread(target=call, args=(h,)) for h in range(nkv)]
+                for t in th:
+                    t.start()
+                for t in th:
+                    t.join()
+            else:
+                for h in range(nkv):
+                    call(h)
+            return O, m, l
+        ref = run(K, V, False)
+        for rep in range(3):
+            got = run(pk.array, pv.array, True)
+            assert all(np.array_equal(a, b) for a, b in zip(got, ref)), f"round {rep}"
+    finally:
+        for w in ws:
+            bb.lib().pa_hip_ws_free(w)
+        pk.close(); pv.close()
+    ex = orc.attn_exact(orc.make_shape(nkv, NR, HD, orc.Q8_0, orc.QMODE_F16, scale=1.0 / 16, rs=rs), Q, K, V, nk)
+    eo, em, el = orc.rel_err(*ref, *ex)
+    assert eo < 2e-3 and em < 2e-3 and el < 2e-3, (eo, em, el)
+
+
 def test_stream_wait_is_bounded():
     """pa_hip_stream_wait, the wait every synchronous call uses: with a 0 ms limit on a stream that still has several
     milliseconds of attention work queued it returns -1 and says so; with a generous limit it returns 0 once the work
@@ -188,3 +225,20 @@ def test_wire_server_big_calls():
     """ATTN_BIG (16 tokens = 2 groups in one engine call) against one-group calls, through the HIP engine."""
     out = run_patool(TOOL_CPU, [16384, 2, 2, 1, 1, 1000, 1024], {"PA_BIG_TOK": 16}, server=SERVE_HIP)
     assert re.search(r"big vs one-group calls: .* -> PASS", out), out
+
+
+@needs_serve
+@pytest.mark.parametrize("helpers", [0, 1])
+def test_wire_server_mixed_engines(helpers):
+    """gpu_permille 500: the reference server gives half of each call's pages to the HIP engine and the other half to its
+    CPU-engine path, which calls the sme_* C ABI of libpa_hip.so while the engine's stream is busy - with sme_helpers 0
+    from four threads at once, one workspace each (sme_page, phone-attn.h:509-520), with 1 through sme_attn_pipe. The
+    two engines' partials are merged by the server (merge_partial, phone-attn.h:231-239); pa-tool's fp64 gate (5e-3) on
+    the normalised reply, held here to 2e-3."""
+    print(f"wire server, mixed engines, sme_helpers={helpers}", flush=True)
+    out = run_patool(TOOL_CPU, [32768, 3, 2, 4, helpers, 500, 1024], {"PA_NTOK": 8}, server=SERVE_HIP)
+    print(out)
+    eo, el, verdict = check_line(out)
+    assert verdict == "PASS" and eo < 2e-3 and el < 2e-3, out
+    m = re.search(r"check call: (\d+) of (\d+) pages on the GPU", out)
+    assert m and 0 < int(m.group(1)) < int(m.group(2)), out
