@@ -10,6 +10,8 @@ namespace pa_hip {
 typedef _Float16 mm_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 mm_h2 __attribute__((ext_vector_type(2)));
 typedef float mm_f16 __attribute__((ext_vector_type(16)));
+typedef int mm_i4 __attribute__((ext_vector_type(4)));
+typedef int mm_i16 __attribute__((ext_vector_type(16)));
 typedef __fp16 mm_tr4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 #define MM_LDS __attribute__((address_space(3)))
 

@@ -15,7 +15,8 @@
 // 32-block for quantized K (quantize_row_q8_0_ref), taken as fp16(d*q*scale*log2 e) so the scores come out in base-2
 // units, and fp16(q) for f16 K (the scale then multiplies the score); PA_QMODE_F16 takes fp16(q*scale) (the reference
 // engines' Qs, phone-attn.h:595-599). Calls over quantized K in the ggml rounding take exact block dots instead (EX
-// below): K staged as its integer quants, three MFMAs per 32-dim block, ggml's per-block scaling in fp32. Online
+// below): q8_0 K staged as its raw int8 quants, one int8 MFMA per 32-dim block (q4_0: its integer quants as fp16, two
+// fp16 MFMAs per block), and ggml's per-block scaling in fp32. Online
 // softmax in base 2 with a reference max that moves only when a score exceeds it by more than 2^MM_PMAX (O is rescaled
 // rarely); the exact max is tracked beside it and applied at the end. The row sum adds the fp16 probabilities the PV
 // MFMAs consume. Output: one split-K slot per workgroup (O unnormalised against the base-2 max, max, sum), folded by
@@ -35,6 +36,8 @@ constexpr int MM_KST = 2 * MM_HD + 16;            // K tile row stride (bytes): 
 constexpr int MM_VST = 2 * MM_HD + 64;            // V tile row stride: the 4 rows x 64 bytes of a half-wave's
                                                   // transposing reads hit distinct banks
 constexpr int MM_KT = 32 * MM_KST, MM_VT = 32 * MM_VST;
+constexpr int MM_KST8 = MM_HD + 16;               // raw int8 K tile row stride (EX == 2): 16 consecutive keys' 16-byte
+                                                  // reads hit distinct banks
 constexpr int MM_KSC = 32 * 8;                    // exact-QK kernels: the tile's K block scales, [key][4 blocks] fp16
 constexpr int MM_STAGE = MM_KT + MM_VT + MM_KSC;
 
@@ -44,7 +47,7 @@ constexpr int MM_STAGE = MM_KT + MM_VT + MM_KSC;
 // (hi, lo) of fp16 values whose sum is the fp16 block scale times scale * log2 e * 2^s_b to about 22 bits (dqb[b]:
 // hi in the low half). s_b puts that product in [8, 16), so neither half overflows or loses bits to subnormals (capped
 // at 14, where the quants' 2^-s_b stays normal).
-template <int FMT, bool PRE, bool EX = false>
+template <int FMT, bool PRE, bool EX>
 __device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32_t row, bool rlive, int h2, mm_h8 (&Qf)[8],
                                           uint32_t (&dqb)[4]) {
     const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * MM_HD + 8 * h2;
@@ -102,6 +105,44 @@ __device__ __forceinline__ void mm_prep_q(const AttnArgs & a, uint32_t h, uint32
     }
 }
 
+// The query rows as the int8 B operand of the exact int8 block dots (EX == 2): lane (h2, n) holds row n's ggml q8_0
+// quants of dims 32b + 16h2 .. +15 (quantize_row_q8_0_ref, as mm_prep_q), and per block b the (hi, lo) fp16 pair whose
+// sum is the fp16 block scale times scale * log2 e (dqb[b], hi in the low half): to about 22 bits where that product
+// is at least 2^-9; below, lo falls into the fp16 subnormals and the pair keeps an absolute error of at most 2^-25, so
+// the block's term dot_b * dk_b * (hi + lo) errs by at most |dot_b| * dk_b * 2^-25 in base-2 units. (The int8 quants
+// cannot carry the 2^-s_b of mm_prep_q.)
+__device__ __forceinline__ void mm_prep_qi8(const AttnArgs & a, uint32_t h, uint32_t row, bool rlive, int h2, pa_u4 (&Qi)[4],
+                                            uint32_t (&dqb)[4]) {
+    const float * qrow = a.q + ((size_t) h * a.rows + (rlive ? row : 0)) * MM_HD + 16 * h2;
+    const uint32_t qmask = rlive ? 0xffffffffu : 0u;
+    const float scale = a.scale;
+    #pragma unroll
+    for (int b = 0; b < 4; b++) {
+        #pragma clang fp contract(off)
+        pa_f4 x[4];
+        #pragma unroll
+        for (int j = 0; j < 4; j++) x[j] = __builtin_bit_cast(pa_f4, __builtin_bit_cast(pa_u4, *(const pa_f4 *) (qrow + 32 * b + 4 * j)) & qmask);
+        float am = 0.0f;
+        #pragma unroll
+        for (int j = 0; j < 4; j++) am = fmaxf(am, fmaxf(fmaxf(fabsf(x[j][0]), fabsf(x[j][1])), fmaxf(fabsf(x[j][2]), fabsf(x[j][3]))));
+        am = mm_max32(am);                                           // the block's other 16 values: lane ^ 32
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const float dq = (float) (_Float16) d * (scale * MM_LOG2E);   // the fp16 block scale * scale, base-2 units
+        const _Float16 hi = (_Float16) dq, lo = (_Float16) (dq - (float) hi);
+        dqb[b] = (uint32_t) __builtin_bit_cast(uint16_t, hi) | ((uint32_t) __builtin_bit_cast(uint16_t, lo) << 16);
+        uint32_t w[4];
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t v = 0;
+            #pragma unroll
+            for (int e = 0; e < 4; e++) v |= ((uint32_t) (int) roundf(x[j][e] * id) & 0xffu) << (8 * e);
+            w[j] = v;
+        }
+        Qi[b] = (pa_u4){w[0], w[1], w[2], w[3]};
+    }
+}
+
 // Row n's result: the sum over both lanes, O rebased from the reference max to the exact one; the final (O, m, l)
 // for a single-chunk call, else split-K slot c
 __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&O)[4], float mref, float mx, float lsum,
@@ -132,20 +173,27 @@ __device__ __forceinline__ void mm_write_out(const AttnArgs & a, const mm_f16 (&
 // PRE: PA_QMODE_GGML over quantized K. Q' then carries scale * log2 e inside its one fp16 rounding, and the QK
 // accumulator starts at -mref, so the MFMAs return the base-2 logit minus the reference max and each probability is a
 // single exp2. Otherwise the scores are scaled and shifted by one fma each.
-// EX: exact block dots, as ggml computes them (PRE only). K is staged as its integer quants (exact in fp16) with the
-// block scales beside the tile, Q as its integer quants times 2^-s_b; per 32-block b the two MFMAs over the block's 32
-// dims give the integer dot times 2^-s_b exactly (products below 2^15, sums below 2^24), and one more MFMA gives
-// dk_b(key) * (hi + lo)(row): dk_b at k = 0 and 1 of A, the row's pair at k = 0 and 1 of B (an outer product in
-// otherwise zero operands), so dk_b * dq_b * scale * log2 e * 2^s_b to about 22 bits. The scores are the fp32 sum over
-// the blocks of these products, started at -mref: ggml's per-block vec_dot arithmetic, with the softmax scale and the
-// base-2 conversion inside each block's factor instead of the dot of two fp16-rounded operands.
+// EX: exact block dots, as ggml computes them (PRE only), in one of two forms.
+//   EX == 1 (q4_0): K is staged as its integer quants (exact in fp16) with the block scales beside the tile, Q as its
+//   integer quants times 2^-s_b; per 32-block b the two fp16 MFMAs over the block's 32 dims give the integer dot times
+//   2^-s_b exactly (products below 2^15, sums below 2^24), and one more MFMA gives dk_b(key) * (hi + lo)(row): dk_b at
+//   k = 0 and 1 of A, the row's pair at k = 0 and 1 of B (an outer product in otherwise zero operands), so
+//   dk_b * dq_b * scale * log2 e * 2^s_b to about 22 bits.
+//   EX == 2 (q8_0): K is staged as its raw int8 quants (no dequantization: half the LDS bytes of the fp16 tile) and Q as
+//   int8 quants; one v_mfma_i32_32x32x32_i8 per block gives the integer dot itself (|dot| < 2^21), converted to fp32
+//   exactly, and the scale product is formed as above from the unscaled pair. Half the QK matrix-core cycles of
+//   EX == 1 for one more VALU conversion per score and block; measured faster on verify and prefill.
+//   Either way the scores are the fp32 sum over the blocks of dot_b * (scale product), started at -mref: ggml's
+//   per-block vec_dot arithmetic, with the softmax scale and the base-2 conversion inside each block's factor instead
+//   of the dot of two fp16-rounded operands.
 // SKIP: a wave whose 32 rows are all past the call's rows only stages (its share of every tile's loads, dequant and LDS
 // stores, and the barriers). For calls with one row block narrower than 32 * NW rows. Without SKIP there is no branch
 // there: one costs 13-20 % on full row blocks, as it separates the next tile's loads from the QK MFMAs, which the
 // compiler otherwise schedules in one basic block.
-template <int FMT, int NW, bool PRE, bool SKIP, bool EX>
+template <int FMT, int NW, bool PRE, bool SKIP, int EX>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) {   // 2 waves per SIMD
     static_assert(!EX || PRE, "exact block dots need ggml's query rounding over quantized K");
+    static_assert(EX != 2 || FMT == 1, "the int8 block dots take q8_0 K");
     constexpr int PF = 2;                                            // tiles whose raw bytes are in flight
     constexpr int NT = 64 * NW;
     constexpr int UPT = 512 / NT;                                    // staging units per thread (512 per tile)
@@ -202,6 +250,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             const int u = tid + NT * i;
             const int tensor = (wave + NW * i) >> 2, key = (u >> 3) & 31, blk = (u >> 1) & 3, half = u & 1;
             pa_u4 lo, hi;
+            if (EX == 2 && tensor == 0) {                            // K: the raw int8 quants, the block scale beside
+                if (half == 0) *(uint16_t *) (st + MM_KT + MM_VT + 8 * key + 2 * blk) = (uint16_t) R[i].d;
+                *(pa_u4 *) (st + key * MM_KST8 + 32 * blk + 16 * half) = R[i].q[0];
+                continue;
+            }
             if (EX && tensor == 0) {                                 // K: integer quants, the block scale beside the tile
                 mm_dequant<FMT, true>(R[i], half, lo, hi);
                 if (half == 0) *(uint16_t *) (st + MM_KT + MM_VT + 8 * key + 2 * blk) = (uint16_t) R[i].d;
@@ -222,7 +275,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
     __builtin_amdgcn_sched_barrier(0);
     mm_h8 Qf[8];
     uint32_t dqb[4] = {0u, 0u, 0u, 0u};
-    mm_prep_q<FMT, PRE, EX>(a, h, row, rlive, h2, Qf, dqb);
+    pa_u4 Qi[4];                                                     // EX == 2: int8 query quants per block
+    if constexpr (EX == 2) mm_prep_qi8(a, h, row, rlive, h2, Qi, dqb);
+    else mm_prep_q<FMT, PRE, EX != 0>(a, h, row, rlive, h2, Qf, dqb);
     // EX: the B operand of the scale products, the (hi, lo) pair of row n at k = 0, 1 (lanes h2 = 0), zero elsewhere
     uint32_t dqw[4];
     #pragma unroll
@@ -269,7 +324,29 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
             const pa_h4 x1 = __builtin_bit_cast(pa_h4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((MM_LDS mm_tr4 *) (vb + 8 * MM_VST)));
             va[db][mi] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
         };
-        if constexpr (EX) {
+        if constexpr (EX == 2) {
+            // per block: the integer dot on the int8 matrix cores (A: key n's quants, dims 32b + 16h2 .. +15, read raw
+            // from the tile; B: the query quants), the scale product as in EX == 1, and dot * product summed in fp32
+            const pa_u2 dk2 = *(const pa_u2 *) (Kt + MM_KT + MM_VT + 8 * n);   // key n's four fp16 block scales
+            const uint32_t hmask = h2 == 0 ? 0xffffffffu : 0u;
+            pa_u4 kq[4];
+            #pragma unroll
+            for (int b = 0; b < 4; b++) kq[b] = *(const pa_u4 *) (Kt + n * MM_KST8 + 32 * b + 16 * h2);
+            #pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const mm_i16 T = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(mm_i4, kq[b]), __builtin_bit_cast(mm_i4, Qi[b]),
+                                                                     (mm_i16){}, 0, 0, 0);
+                const uint32_t dkw = pa_perm(0u, dk2[b >> 1], (b & 1) ? 0x03020302u : 0x01000100u) & hmask;
+                const mm_f16 Pb = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mm_h8, (pa_u4){dkw, 0u, 0u, 0u}),
+                                                                         __builtin_bit_cast(mm_h8, (pa_u4){dqw[b], 0u, 0u, 0u}),
+                                                                         (mm_f16){}, 0, 0, 0);
+                #pragma unroll
+                for (int v = 0; v < 16; v++) S[v] = fmaf(Pb[v], (float) T[v], b == 0 ? -mc : S[v]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            #pragma unroll
+            for (int kk = 0; kk < 8; kk++) v_read(kk);               // V^T after the block dots, under the softmax
+        } else if constexpr (EX) {
             // per block: the integer dot times 2^-s_b (two MFMAs, exact), the products dk_b(key) * (hi + lo) (one MFMA:
             // dk_b at k = 0 and 1, so dk_b * dq_b * scale * log2 e * 2^s_b to about 22 bits), their fp32 product summed
             // over the blocks in block order from -mref: the base-2 logit minus the reference max
@@ -380,14 +457,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mma_kernel(const AttnArgs a) 
 template <int FMT, bool PRE>
 static hipError_t launch_mma_fmt(int nw, bool skip, const AttnArgs & a, uint32_t grid, hipStream_t st, hipEvent_t ev0,
                                  hipEvent_t ev1) {
+    constexpr int EXF = !PRE ? 0 : FMT == 1 ? 2 : 1;                 // exact block dots: int8 for q8_0, fp16 for q4_0
     switch (nw) {
         case 4:
-            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, true, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
-            else hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, false, PRE>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
+            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, true, EXF>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
+            else hipExtLaunchKernelGGL((mma_kernel<FMT, 4, PRE, false, EXF>), dim3(grid), dim3(256), 0, st, ev0, ev1, 0, a);
             break;
         case 8:
-            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, true, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
-            else hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, false, PRE>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            if (skip) hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, true, EXF>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
+            else hipExtLaunchKernelGGL((mma_kernel<FMT, 8, PRE, false, EXF>), dim3(grid), dim3(512), 0, st, ev0, ev1, 0, a);
             break;
         default: return hipErrorInvalidValue;
     }
