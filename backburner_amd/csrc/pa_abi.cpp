@@ -264,6 +264,15 @@ void page_table(AttnArgs & a, const void * const * k_pages, const void * const *
     a.pstart[np] = acc;
     a.cstart[np] = tacc;
     a.n_pages = (uint32_t) np;
+    // uniform pages: every page but the last holds the same power of two of whole 32-key tiles
+    a.ptl = 32u;
+    if (np == 1) a.ptl = 31u;
+    else if (nkeys[p0] % 32 == 0 && nkeys[p0] > 0) {
+        const uint32_t t = nkeys[p0] / 32;
+        bool same = (t & (t - 1)) == 0;
+        for (int i = 1; same && i + 1 < np; i++) same = nkeys[p0 + i] == nkeys[p0];
+        if (same) a.ptl = (uint32_t) __builtin_ctz(t);
+    }
 }
 
 // With a fixed slot array: the most chunks per launch that let every launch's slots fit (0 if none would), given the

@@ -16,6 +16,8 @@ struct AttnArgs {
     const uint8_t * vp[MAXP];
     uint32_t pstart[MAXP + 1];      // key prefix: page p holds keys [pstart[p], pstart[p+1]) of the call
     uint32_t cstart[MAXP + 1];      // decode kernel: 32-key tile prefix, page p holds tiles [cstart[p], cstart[p+1])
+    uint32_t ptl;                   // log2 of the tiles per page when every page but the last holds that same power of
+                                    // two of 32-key tiles (the last one any number), else 32: pages by shift, no table walk
     uint32_t n_pages, n_chunks, chunk, n_items;   // chunk = keys per workgroup; n_items = chunks x heads x row blocks
                                                   // (decode kernel: n_chunks = tile groups, chunk = 32, items = groups x pairs)
     uint32_t rs, hb, nkv;

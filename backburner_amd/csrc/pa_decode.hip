@@ -206,7 +206,16 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
         const int q = 64 * i + lane;
         vo[i] = q < TCH ? (uint32_t) (q / G::NCH) * rs + 16u * (uint32_t) (q % G::NCH) : 0x80000000u;
     }
-    auto page_of = [&](uint32_t tau, uint32_t & pg) { while (a.cstart[pg + 1] <= tau) pg++; };   // pages only advance
+    // the page of tile tau, its first tile and its key count: by shift for uniform pages (a.ptl < 32), else by a walk of
+    // the page table (pages only advance); the scalar loads of the walk wait for the LDS operations in flight too
+    const uint32_t ptl = a.ptl, np1 = a.n_pages - 1;
+    const uint32_t last_keys = a.pstart[a.n_pages] - a.pstart[np1];
+    auto page_of = [&](uint32_t tau, uint32_t & pg) {
+        if (ptl < 32u) pg = min(tau >> ptl, np1);
+        else while (a.cstart[pg + 1] <= tau) pg++;
+    };
+    auto page_tile0 = [&](uint32_t pg) { return ptl < 32u ? pg << ptl : a.cstart[pg]; };
+    auto page_keys = [&](uint32_t pg) { return ptl < 32u ? (pg < np1 ? 32u << ptl : last_keys) : a.pstart[pg + 1] - a.pstart[pg]; };
     auto tile_load = [&](pa_u4 (&X)[CPL], uint32_t pg, uint32_t j0, uint32_t nrec) {   // rows j0 .. of page pg
         const uint8_t * tb = (hd ? a.vp[pg] : a.kp[pg]) + (size_t) pr * G::SL + (size_t) j0 * rs;
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *) tb, (short) 0, (int) nrec, 0x00020000);
@@ -239,10 +248,10 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
     auto load_tile = [&](pa_u4 (&X)[CPL], uint32_t tau) {            // tile tau, or (past the end) an empty range
         if (tau < T) {
             page_of(tau, pl);
-            const uint32_t j0 = 32 * (tau - a.cstart[pl]);
+            const uint32_t j0 = 32 * (tau - page_tile0(pl));
             // the range covers the tile's rows only (at most 32 of rs bytes, rs < 2^26 by the host's check), so a page
             // of any size keeps the 32-bit byte count exact; the pair's slice ends inside each row (nkv * hb <= rs)
-            tile_load(X, pl, j0, min(a.pstart[pl + 1] - a.pstart[pl] - j0, 32u) * rs - pr * G::SL);
+            tile_load(X, pl, j0, min(page_keys(pl) - j0, 32u) * rs - pr * G::SL);
         } else {
             tile_load(X, pl, 0, 0u);
         }
@@ -316,7 +325,7 @@ __global__ __launch_bounds__(128, 2) void dec_kernel(const AttnArgs a) {
         // ---- the tile's raw pair slices -> LDS (this wave's tensor), then this register set's next tile (DEC_PF steps
         // ahead; past the last one an empty range that loads nothing)
         page_of(tau, pc);
-        const int nvalid = (int) min(32u, a.pstart[pc + 1] - a.pstart[pc] - 32 * (tau - a.cstart[pc]));
+        const int nvalid = (int) min(32u, page_keys(pc) - 32 * (tau - page_tile0(pc)));
         dec_lds_barrier();                                           // both waves are done reading the previous tile
         tile_store(X);
         load_tile(X, tau + DEC_PF * NG);
