@@ -384,20 +384,20 @@ def main():
         extra["prefill"] = workload(
             bb, ws, args, "prefill", bb.FMT_Q8_0, nl, 65536, 4096,
             f"prefill chunk: 512 tokens x 64 q-heads / 8 kv-heads (4096 rows per KV head), hd 128, 65536 q8_0 keys, "
-            f"{nl} distinct caches", "mfma", "pa_hip::mma_kernel<1, 8, true, false, 2> (q8_0 prefill, exact int8 block dots)",
+            f"{nl} distinct caches", "mfma", "pa_hip::mma_kernel<1, 8, false, true> (q8_0 prefill, exact int8 block dots)",
             max(1, min(args.steps, 3)), 1, pmc="prefill", outliers=0)
     if want("prefill_f16"):
         extra["prefill_f16"] = workload(
             bb, ws, args, "prefill_f16", bb.FMT_Q8_0, nl, 65536, 4096,
             f"prefill chunk as above in the reference engines' rounding: queries f16(q*scale), K/V dequantized to fp16 in "
             f"LDS, fp16 MFMA with fp32 accumulation (the Metal engine's arithmetic), {nl} distinct caches", "mfma",
-            "pa_hip::mma_kernel<1, 8, false, false, 0> (q8_0 prefill, fp16 operands)",
+            "pa_hip::mma_kernel<1, 8, false, false> (q8_0 prefill, fp16 operands)",
             max(1, min(args.steps, 3)), 0, pmc="prefill_f16", outliers=0, qmode=bb.QMODE_F16)
     if want("verify"):
         extra["verify"] = workload(
             bb, ws, args, "verify", bb.FMT_Q8_0, nl, 98304, 128,
             f"draft-block verify: 16 tokens x 64 q-heads / 8 kv-heads (128 rows per KV head), hd 128, 98304 q8_0 keys, "
-            f"{nl} layers", "hbm", "pa_hip::mma_kernel<1, 4, true, false, 2> (q8_0 verify, exact int8 block dots)",
+            f"{nl} layers", "hbm", "pa_hip::mma_kernel<1, 4, false, true> (q8_0 verify, exact int8 block dots)",
             max(2, min(args.steps, 10)), 4, pmc="verify", outliers=0)
     if want("decode_q4_0"):
         extra["decode_q4_0"] = workload(
@@ -408,7 +408,7 @@ def main():
         extra["verify_q4_0"] = workload(
             bb, ws, args, "verify_q4_0", bb.FMT_Q4_0, nl, 143360, 128,
             f"verify 16 tokens, 8 kv-heads x 128 rows, hd 128, 143360 q4_0 keys, {nl} layers", "mfma",
-            "pa_hip::mma_kernel<2, 4, true, false, 1> (q4_0 verify, exact block dots)", max(2, min(args.steps, 10)), 2, outliers=0)
+            "pa_hip::mma_kernel<2, 4, false, true> (q4_0 verify, exact int8 block dots)", max(2, min(args.steps, 10)), 2, outliers=0)
     if want("decode_4096"):
         extra["decode_4096"] = workload(
             bb, ws, args, "decode_4096", bb.FMT_Q8_0, 1, 4096, 8,

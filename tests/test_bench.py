@@ -36,9 +36,9 @@ def test_committed_traffic_summary():
     assert "dec_kernel" in (ROOT / "profiles" / "bench_all_kernels.md").read_text()
 
 
-@pytest.mark.parametrize("name,kernel,flop", [("prefill", "mma_kernel<1, 8, true, false, 2>", 4 * 4096 * 65536 * 128 * 8),
-                                              ("prefill_f16", "mma_kernel<1, 8, false, false, 0>", 4 * 4096 * 65536 * 128 * 8),
-                                              ("verify", "mma_kernel<1, 4, true, false, 2>", 4 * 128 * 98304 * 128 * 8),
+@pytest.mark.parametrize("name,kernel,flop", [("prefill", "mma_kernel<1, 8, false, true>", 4 * 4096 * 65536 * 128 * 8),
+                                              ("prefill_f16", "mma_kernel<1, 8, false, false>", 4 * 4096 * 65536 * 128 * 8),
+                                              ("verify", "mma_kernel<1, 4, false, true>", 4 * 128 * 98304 * 128 * 8),
                                               ("reference_shape", "mma256_kernel<256, 1, true, false, 2>", 4 * 48 * 65536 * 256 * 4)])
 def test_committed_mma_counters(name, kernel, flop):
     """The matrix-core kernels' counter summaries: the MFMA work the counters saw (fp16 MOPS_F16 x 512 plus int8
@@ -52,7 +52,7 @@ def test_committed_mma_counters(name, kernel, flop):
     assert c.get("int8_mfma_ops", 0) == c["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
     work = c["fp16_mfma_flops"] + c.get("int8_mfma_ops", 0)
     assert flop <= work <= 1.3 * flop
-    if kernel.endswith(", 2>") and name != "reference_shape":          # int8 QK: exactly half the algorithmic work
+    if kernel.endswith("false, true>"):                                # int8 QK: exactly half the algorithmic work
         assert c["int8_mfma_ops"] == flop // 2
     assert d["alg_bytes_per_launch"] <= d["traffic_bytes_per_launch"] < 1.6 * d["alg_bytes_per_launch"]
     assert 0 < c["mfma_busy_frac"] < 1 and 0 < c["MfmaUtil_pct"] < 100
