@@ -107,7 +107,7 @@ void pa_hip_ws_destroy(pa_hip_ws * ws);
 /* Split-K geometry of this workspace's calls, for tests and tuning (no counterpart in the reference: the Metal engine
  * fixes its chunking, pa-metal.mm:627-646). decode_groups > 0: tile groups per head pair and launch of the decode
  * kernel (<= 8 rows, head dim 128); mma_workgroups > 0: workgroups per launch of the other kernels; 0 restores the
- * default (about 1024 decode workgroups, one round of resident workgroups otherwise). Returns 0 or -1. */
+ * default (one round of resident workgroups: 768 decode workgroups for q8_0, 1024 for q4_0). Returns 0 or -1. */
 int pa_hip_ws_set_split(pa_hip_ws * ws, int decode_groups, int mma_workgroups);
 
 /* config_req.gpu_chunk (phone-attn.h:88-89, "keys per GPU threadgroup"; the Metal engine's chunk, pa-metal.mm:842): each
