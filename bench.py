@@ -403,12 +403,13 @@ def main():
         extra["decode_q4_0"] = workload(
             bb, ws, args, "decode_q4_0", bb.FMT_Q4_0, nl, 143360, 8,
             f"decode 1 token, 8 kv-heads x 8 rows, hd 128, 143360 q4_0 keys, {nl} layers", "hbm",
-            "pa_hip::dec_kernel<2> (q4_0 decode)", args.steps, 16, outliers=0)
+            "pa_hip::dec_kernel<2> (q4_0 decode)", args.steps, 16, outliers=0, pmc="decode_q4_0")
     if want("verify_q4_0"):
         extra["verify_q4_0"] = workload(
             bb, ws, args, "verify_q4_0", bb.FMT_Q4_0, nl, 143360, 128,
             f"verify 16 tokens, 8 kv-heads x 128 rows, hd 128, 143360 q4_0 keys, {nl} layers", "mfma",
-            "pa_hip::mma_kernel<2, 4, false, true> (q4_0 verify, exact int8 block dots)", max(2, min(args.steps, 10)), 2, outliers=0)
+            "pa_hip::mma_kernel<2, 4, false, true> (q4_0 verify, exact int8 block dots)", max(2, min(args.steps, 10)), 2, outliers=0,
+            pmc="verify_q4_0")
     if want("decode_4096"):
         extra["decode_4096"] = workload(
             bb, ws, args, "decode_4096", bb.FMT_Q8_0, 1, 4096, 8,
