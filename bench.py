@@ -350,7 +350,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--only", default="", help="comma list of the extra workloads to run (prefill, prefill_f16, verify, "
                                                 "decode_q4_0, verify_q4_0, decode_4096, reference_shape, accept); default all")
-    ap.add_argument("--secondary", action="store_true", help="also run the reply side, KV ingest and the head-dim-256 shape")
+    ap.add_argument("--secondary", action="store_true", help="also run the reply side, KV ingest and the head-dim-256 shape in ggml's rounding")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-layers", type=int, default=16, help="layers of the headline workload the CPU baseline runs")
     args = ap.parse_args()
