@@ -111,9 +111,8 @@ void pa_hip_ws_destroy(pa_hip_ws * ws);
 int pa_hip_ws_set_split(pa_hip_ws * ws, int decode_groups, int mma_workgroups);
 
 /* config_req.gpu_chunk (phone-attn.h:88-89, "keys per GPU threadgroup"; the Metal engine's chunk, pa-metal.mm:842): each
- * workgroup of this workspace's calls takes a split-K chunk of about `keys` keys (rounded to the kernel's 32-key tiles,
- * or to the head-dim-256 generic kernel's key block); 0 restores the default geometry. pa_hip_ws_set_split's counts, when
- * set, take precedence. Returns 0 or -1. */
+ * workgroup of this workspace's calls takes a split-K chunk of about `keys` keys (rounded to the kernels' 32-key tiles);
+ * 0 restores the default geometry. pa_hip_ws_set_split's counts, when set, take precedence. Returns 0 or -1. */
 int pa_hip_ws_set_chunk_keys(pa_hip_ws * ws, uint32_t keys);
 
 /* engine::alloc_page / free_page (phone-attn.h:168-169): K and V storage of one page in HBM (device pointers, 256-byte
