@@ -3,7 +3,8 @@ against pa_hip_attn on the same inputs, through the C ABI: two calls in a row, t
 over 98,304 q8_0 keys, then a one-token decode over 4,096 keys), each equal to pa_hip_attn's output bit for bit (the
 same split) and within the 2e-3 parity bar of the oracle; a call over 130 pages (three launches) whose default split
 would overflow the scratch, with the split adapted to fit (within the bar of pa_hip_attn's output and of the oracle);
-and a call whose launches cannot each hold one split, refused with an error before anything is enqueued."""
+a call whose launches cannot each hold one split, refused with an error before anything is enqueued; and the call
+captured in a HIP graph, every replay equal to the eager call."""
 import numpy as np
 import pytest
 
@@ -97,6 +98,51 @@ def test_noalloc_adapts_split_to_scratch():
         assert eo < TOL and em < TOL and el < TOL
     finally:
         kbuf.close(); vbuf.close(); ws.close()
+
+
+@pytest.mark.parametrize("fmt,nkv,rows,nk", [(bb.FMT_Q8_0, 8, 8, 8192), (bb.FMT_Q4_0, 8, 128, 3000)])
+def test_noalloc_graph_replays(fmt, nkv, rows, nk):
+    """The callers the entry point is for include code under HIP graph capture: a captured pa_hip_attn_noalloc call
+    (split-K partials in the fixed scratch, no allocation, no memset), replayed four times over a poisoned output with an
+    eager call of another problem in between (which reuses the same scratch), equals the eager call bit for bit."""
+    print(f"noalloc graph: fmt={fmt} nkv={nkv} rows={rows} nk={nk}", flush=True)
+    syn = bb.synth()
+    kbuf, vbuf, Q, pages, shape = make(fmt, nkv, rows, nk, 7401 + rows)
+    Q2 = orc.normal(7501 + rows, 0, nkv * rows * 128).reshape(-1, 128)
+    n = nkv * rows
+    stream = syn.pa_synth_stream_new()
+    dq, dq2 = bb.DeviceBuffer.from_array(Q), bb.DeviceBuffer.from_array(Q2)
+    out, out2 = bb.DeviceBuffer(n * 128 * 4 + n * 8), bb.DeviceBuffer(n * 128 * 4 + n * 8)
+
+    def call(q, o):
+        bb.attn_noalloc(shape, pages, q.ptr, o.ptr, o.ptr + n * 128 * 4, o.ptr + n * 128 * 4 + n * 4, stream)
+
+    gx = None
+    try:
+        call(dq, out)                                                # eager (the first call also looks up the scratch)
+        assert syn.pa_synth_stream_sync(stream) == 0
+        want = out.download(np.uint8)
+        call(dq2, out2)
+        assert syn.pa_synth_stream_sync(stream) == 0
+        other = out2.download(np.uint8)
+        assert not np.array_equal(want, other)
+        assert syn.pa_synth_capture_begin(stream) == 0
+        call(dq, out)
+        gx = syn.pa_synth_capture_end(stream)
+        assert gx, "capture failed"
+        for rep in range(4):
+            out.upload(np.full(n * 128 * 4 + n * 8, 0x7f, np.uint8))  # poison: every replay must write everything
+            assert syn.pa_synth_graph_launch(gx, stream) == 0
+            assert syn.pa_synth_stream_sync(stream) == 0
+            assert np.array_equal(out.download(np.uint8), want), f"replay {rep} differs from the eager call"
+            call(dq2, out2)                                          # eager work on the same scratch between replays
+            assert syn.pa_synth_stream_sync(stream) == 0
+            assert np.array_equal(out2.download(np.uint8), other)
+    finally:
+        if gx:
+            syn.pa_synth_graph_free(gx)
+        for x in (dq, dq2, out, out2, kbuf, vbuf):
+            x.close()
 
 
 def test_noalloc_refuses_what_cannot_fit():
