@@ -27,49 +27,73 @@ __device__ __forceinline__ void merge_write_reply(const MergeArgs & a, size_t of
     }
 }
 
-// Used when one call needs several attention launches (more than MAXP pages). One workgroup per output row; thread t
-// folds dims 4*(t % (HD/4)) over slots t / (HD/4), t / (HD/4) + SG, ...
+// More slots than one workgroup's lanes hold (calls of several launches: more than MAXP pages): one workgroup of 256
+// threads per (row, 32 dims), as the wide merge below, over the slots in batches of 256 - first the max over every
+// batch's (max, sum) pairs, then per batch the wide merge's loads (eight lanes per slot line, the batch's loads issued
+// at once), weighed by that max and summed.
 template <int HD>
-__global__ __launch_bounds__(256) void merge_kernel(const MergeArgs a) {
-    constexpr int TPR = HD / 4, SG = 256 / TPR;
-    __shared__ pa_f4 red[SG][TPR];
-    __shared__ float redl[SG];
-    __shared__ float redm[256];
-    const uint32_t r = blockIdx.x;                   // output row = h*rows + i
+__global__ __launch_bounds__(256) void merge_batched_kernel(const MergeArgs a) {
+    constexpr int NQ = HD / 32, NT = 256, NWV = NT / 64;
+    __shared__ float sM[NWV], sL[NWV];
+    __shared__ pa_f4 sA[NWV][8];
+    const uint32_t r = blockIdx.x / NQ, dq = blockIdx.x % NQ;   // output row h*rows + i, dims 32 dq .. +31
     const uint32_t h = r / a.rows, i = r % a.rows;
-    const int t = threadIdx.x, d4 = t % TPR, sg = t / TPR;
-    const size_t pr = ((size_t) h * a.qr + i) * a.rst;              // slot s at s * a.sst + pr
+    const int t = threadIdx.x, lane = t % 64, wv = t / 64;
+    const size_t pr = ((size_t) h * a.qr + i) * a.rst;              // slot s of the row at s * a.sst + pr
+    const uint32_t nb = (a.n_slots + NT - 1) / NT;
     float M = -INFINITY;
-    for (uint32_t s = t; s < a.n_slots; s += 256) M = fmaxf(M, a.pml[s * a.sst + pr].x);
-    redm[t] = M;
-    __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (t < off) redm[t] = fmaxf(redm[t], redm[t + off]);
-        __syncthreads();
+    for (uint32_t b = 0; b < nb; b++) {
+        const uint32_t s = b * NT + t;
+        if (s < a.n_slots) M = fmaxf(M, a.pml[s * a.sst + pr].x);
     }
-    M = redm[0];
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) sM[wv] = M;
+    __syncthreads();
+    #pragma unroll
+    for (int k = 0; k < NWV; k++) M = fmaxf(M, sM[k]);
     const float Ms = M == -INFINITY ? 0.0f : M;
     pa_f4 acc = {0.f, 0.f, 0.f, 0.f};
     float L = 0.0f;
-    for (uint32_t s = sg; s < a.n_slots; s += SG) {
-        const float2 ml = a.pml[s * a.sst + pr];
-        const float w = __builtin_amdgcn_exp2f(ml.x - Ms);   // ml.x = -inf -> 0 (an empty slot)
-        L += w * ml.y;
-        acc += w * *(const pa_f4 *) (a.po + (s * a.sst + pr) * HD + 4 * d4);
-    }
-    red[sg][d4] = acc;
-    if (d4 == 0) redl[sg] = L;
-    __syncthreads();
-    if (sg == 0) {
-        for (int q = 1; q < SG; q++) acc += red[q][d4];
-        for (int q = 1; q < SG; q++) L += redl[q];                    // every thread: the reply needs L
-        if (a.Oh) {
-            const float ov[4] = {acc[0], acc[1], acc[2], acc[3]};
-            merge_write_reply<4>(a, (size_t) r * HD + 4 * d4, ov, M, L, r, d4 == 0);
-            return;
+    for (uint32_t b = 0; b < nb; b++) {
+        pa_f4 o[8];
+        #pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t s = b * NT + 64 * wv + lane / 8 + 8 * j;
+            o[j] = s < a.n_slots ? *(const pa_f4 *) (a.po + (s * a.sst + pr) * HD + 32 * dq + 4 * (lane % 8))
+                                 : (pa_f4){0.f, 0.f, 0.f, 0.f};
         }
-        *(pa_f4 *) (a.O + (size_t) r * HD + 4 * d4) = acc;
-        if (d4 == 0) { a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2; a.l[r] = L; }
+        const uint32_t st = b * NT + t;
+        const float2 ml = st < a.n_slots ? a.pml[st * a.sst + pr] : make_float2(-INFINITY, 0.0f);
+        const float w = __builtin_amdgcn_exp2f(ml.x - Ms);          // -inf (an empty or absent slot) -> 0
+        L += w * ml.y;
+        #pragma unroll
+        for (int j = 0; j < 8; j++) acc += __shfl(w, lane / 8 + 8 * j) * o[j];   // slot's weight: this wave's lane
+    }
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+    #pragma unroll
+    for (int off = 8; off < 64; off <<= 1)
+        #pragma unroll
+        for (int k = 0; k < 4; k++) acc[k] += __shfl_xor(acc[k], off);
+    if (lane < 8) sA[wv][lane] = acc;
+    if (lane == 0) sL[wv] = L;
+    __syncthreads();
+    if (wv != 0 || lane >= 8) return;
+    acc = sA[0][lane];
+    L = sL[0];
+    #pragma unroll
+    for (int k = 1; k < NWV; k++) { acc += sA[k][lane]; L += sL[k]; }
+    const size_t off = (size_t) r * HD + 32 * dq + 4 * lane;        // lanes 0-7 of wave 0: dims 32 dq + 4 lane .. +3
+    if (a.Oh) {
+        const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+        merge_write_reply<4>(a, off, v, M, L, r, dq == 0 && lane == 0);
+        return;
+    }
+    *(pa_f4 *) (a.O + off) = acc;
+    if (dq == 0 && lane == 0) {
+        a.m[r] = M == -INFINITY ? -INFINITY : M * PA_LN2;
+        a.l[r] = L;
     }
 }
 
@@ -206,8 +230,8 @@ hipError_t launch_merge(int hd, const MergeArgs & a, hipStream_t st) {
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }
-    if (hd == 128) hipLaunchKernelGGL(merge_kernel<128>, dim3(grid), dim3(256), 0, st, a);
-    else if (hd == 256) hipLaunchKernelGGL(merge_kernel<256>, dim3(grid), dim3(256), 0, st, a);
+    if (hd == 128) hipLaunchKernelGGL((merge_batched_kernel<128>), dim3(grid * 4), dim3(256), 0, st, a);
+    else if (hd == 256) hipLaunchKernelGGL((merge_batched_kernel<256>), dim3(grid * 8), dim3(256), 0, st, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

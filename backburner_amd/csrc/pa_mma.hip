@@ -19,7 +19,7 @@
 // fp32. Online softmax in base 2 with a reference max that moves only when a score exceeds it by more than 2^MM_PMAX (O is rescaled
 // rarely); the exact max is tracked beside it and applied at the end. The row sum adds the fp16 probabilities the PV
 // MFMAs consume. Output: one split-K slot per workgroup (O unnormalised against the base-2 max, max, sum), folded by
-// merge_kernel, or the final (O, m, l) when the call has a single chunk.
+// the merge kernels, or the final (O, m, l) when the call has a single chunk.
 //
 // Reference roles: pa_attn_big + pa_big_load (pa-metal.mm:379-487: per (row tile, KV head, key chunk) dequantize a
 // K/V block into threadgroup memory as half, S = QK^T on the matrix units, online softmax with key masking, O = a O +
