@@ -9,7 +9,8 @@
 
 namespace pa_hip {
 
-constexpr int MAXP = 64;   // pages per attention launch (more are split over several launches into one slot array)
+constexpr int MAXP = 128;  // pages per attention launch (more are split over several launches into one slot array): 512k
+                           // keys in 4,096-key pages, with the kernel arguments under 4 KB
 
 struct AttnArgs {
     const uint8_t * kp[MAXP];       // page base (key 0, head 0) of K / V
@@ -35,6 +36,7 @@ struct AttnArgs {
     float2 * pml;                   // the same without hd: (max in base-2 units, sum)
     float * O, * m, * l;            // final [nkv][rows][hd], [nkv][rows]
 };
+static_assert(sizeof(AttnArgs) <= 4096, "the page table travels in the kernel arguments");
 
 struct MergeArgs {
     const float * po;

@@ -131,7 +131,7 @@ int pa_hip_attn(pa_hip_ws * ws, const pa_hip_shape * shape, const void * const *
  * capture, serving loops that forbid hipMalloc). The same arguments without a workspace; the call's split-K partials go
  * to a fixed device array of PA_HIP_NOALLOC_SCRATCH bytes that each GPU holds from its first such call until the
  * process ends, and the call allocates nothing. The split adapts so the partials fit (a single launch always does);
- * a call over more than 64 pages whose launches cannot each hold one split of the rows is refused (-1). Every call on
+ * a call over more than 128 pages whose launches cannot each hold one split of the rows is refused (-1). Every call on
  * one GPU shares that GPU's array: calls that overlap on one GPU race (order them on one stream). Returns 0 once
  * enqueued, -1 on a bad argument (nothing enqueued). */
 #define PA_HIP_NOALLOC_SCRATCH (64u << 20)

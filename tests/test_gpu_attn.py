@@ -111,10 +111,10 @@ def test_outlier_channels_and_padding(ws):
     run_and_check(ws, bb.FMT_Q8_0, 8, 8, 128, 2048, seed=31, rs_pad=16, outliers=4)
 
 
-@pytest.mark.parametrize("pages", [[3, 0, 64, 1, 130], [1], [4096, 4096, 17], [10] * 70, [1024, 1024, 1024, 5000], [64] * 70,
+@pytest.mark.parametrize("pages", [[3, 0, 64, 1, 130], [1], [4096, 4096, 17], [10] * 140, [1024, 1024, 1024, 5000], [64] * 140,
                                    [96, 96, 96], [512, 1024, 512]])
 def test_ragged_pages(ws, pages):
-    """Uneven page sizes, empty pages, single keys and more pages than one launch holds (70 > 64); equal power-of-two
+    """Uneven page sizes, empty pages, single keys and more pages than one launch holds (140 > 128); equal power-of-two
     pages (found by shift in the decode kernel) with a shorter or a longer last page, in one launch and over two, and
     equal pages that are not a power of two of tiles or a longer page in the middle (found by the page-table walk)."""
     run_and_check(ws, bb.FMT_Q8_0, 2, 8, 128, sum(pages), seed=5 + len(pages), page_keys=pages)

@@ -8,7 +8,7 @@ O, m and l; orc_attn_ggml in PA_QMODE_GGML):
   row block at all keys, with plain and with x8 outlier-channel keys, and in the reference engines' rounding
   (f16 queries, fp16-dequantized K/V) against the fp64 form;
 - the 16-token verify at 98,304 keys with x8 outlier-channel keys;
-- more than 256 split-K slots (a decode over 65 pages: two launches, 272 slots, the generic merge);
+- more than 256 split-K slots (a decode over 129 pages: two launches, 272 slots, the batched merge);
 - pages whose byte size exceeds 2^32 (rows of 4,352 bytes, 2^20 + 100 keys), through the decode and the matrix-core
   kernels;
 - head dim 256 calls small enough for a single chunk (the kernel writes the result itself), and the
@@ -153,11 +153,11 @@ def test_verify_full_size_outlier_keys(ws, fmt, nk):
 
 @pytest.mark.parametrize("rows", [8, 128])
 def test_more_than_256_slots(ws, rows):
-    """65 pages of 1,024 keys: two launches. Decode with 256 tile groups per head pair (the q4_0 default; set here for
-    q8_0): 256 + 16 = 272 split-K slots per row (the generic merge kernel); verify: 64 + 32 chunks (the wide merge over
-    96 slots)."""
-    print(f"65 pages, rows={rows}", flush=True)
-    c = DevCase(bb.FMT_Q8_0, 8, rows, 65 * 1024, 4401 + rows, page_keys=1024)
+    """129 pages of 512 keys: two launches (128 pages, then 1). Decode with 256 tile groups per head pair (the q4_0
+    default; set here for q8_0): 256 + 16 = 272 split-K slots per row (the batched merge); verify: 64 + 16 chunks (the
+    wide merge over 80 slots)."""
+    print(f"129 pages, rows={rows}", flush=True)
+    c = DevCase(bb.FMT_Q8_0, 8, rows, 129 * 512, 4401 + rows, page_keys=512)
     try:
         if rows == 8:
             ws.set_split(decode_groups=256)
@@ -166,7 +166,7 @@ def test_more_than_256_slots(ws, rows):
         finally:
             ws.set_split()
         sel = np.arange(rows) if rows == 8 else np.arange(1, rows, 8)
-        check(f"65 pages rows={rows}", pick(out, 8, rows, sel), c.oracle(sel))
+        check(f"129 pages rows={rows}", pick(out, 8, rows, sel), c.oracle(sel))
     finally:
         c.close()
 

@@ -1,7 +1,7 @@
 """pa_hip_attn_noalloc (the engine call that allocates nothing: split-K partials in the library's fixed per-GPU scratch)
 against pa_hip_attn on the same inputs, through the C ABI: two calls in a row, the second smaller (a 16-token verify
 over 98,304 q8_0 keys, then a one-token decode over 4,096 keys), each equal to pa_hip_attn's output bit for bit (the
-same split) and within the 2e-3 parity bar of the oracle; a call over 130 pages (three launches) whose default split
+same split) and within the 2e-3 parity bar of the oracle; a call over 258 pages (three launches) whose default split
 would overflow the scratch, with the split adapted to fit (within the bar of pa_hip_attn's output and of the oracle);
 a call whose launches cannot each hold one split, refused with an error before anything is enqueued; and the call
 captured in a HIP graph, every replay equal to the eager call."""
@@ -78,11 +78,12 @@ def test_noalloc_matches_attn_two_calls():
 
 
 def test_noalloc_adapts_split_to_scratch():
-    """130 pages of 1,024 keys (three launches of the verify kernel): the default 64 chunks per launch of 128 rows x 8
-    heads would need 102 MB of partials, more than the 64 MiB scratch; the call takes 42 chunks per launch instead."""
-    print("noalloc: 130 pages, verify rows", flush=True)
+    """258 pages of 512 keys (three launches of the verify kernel: 128, 128 and 2 pages): the default 64 chunks per
+    launch of 128 rows x 8 heads would need 102 MB of partials, more than the 64 MiB scratch; the call takes 42 chunks
+    per launch instead."""
+    print("noalloc: 258 pages, verify rows", flush=True)
     ws = bb.Workspace()
-    kbuf, vbuf, Q, pages, shape = make(bb.FMT_Q8_0, 8, 128, 130 * 1024, 7301, page_keys=1024)
+    kbuf, vbuf, Q, pages, shape = make(bb.FMT_Q8_0, 8, 128, 258 * 512, 7301, page_keys=512)
     try:
         got, want = both(shape, pages, Q, ws)
         eo, em, el = orc.rel_err(*got, *want)
@@ -92,7 +93,7 @@ def test_noalloc_adapts_split_to_scratch():
         idx = (np.arange(8)[:, None] * 128 + sel[None, :]).reshape(-1)
         qs = Q.reshape(8, 128, 128)[:, sel, :].reshape(-1, 128)
         ref = orc.attn_ggml(orc.make_shape(8, len(sel), 128, bb.FMT_Q8_0), qs, kbuf.download(np.uint8), vbuf.download(np.uint8),
-                            130 * 1024)
+                            258 * 512)
         eo, em, el = orc.rel_err(got[0][idx], got[1][idx], got[2][idx], *ref)
         print(f"  vs oracle: O {eo:.2e} m {em:.2e} l {el:.2e}", flush=True)
         assert eo < TOL and em < TOL and el < TOL
@@ -146,7 +147,7 @@ def test_noalloc_graph_replays(fmt, nkv, rows, nk):
 
 
 def test_noalloc_refuses_what_cannot_fit():
-    """193 pages (four launches) of 4,096 rows x 8 heads: one split per launch already needs 4 x 17 MB of partials; the
+    """385 pages (four launches) of 4,096 rows x 8 heads: one split per launch already needs 4 x 17 MB of partials; the
     host refuses the call before enqueueing anything (the pages are real memory: one 32-key buffer shared by all)."""
     nkv, rows = 8, 4096
     rs = nkv * bb.head_bytes(bb.FMT_Q8_0, 128)
@@ -154,7 +155,7 @@ def test_noalloc_refuses_what_cannot_fit():
     n = nkv * rows
     dq, do, dml = bb.DeviceBuffer(n * 128 * 4), bb.DeviceBuffer(n * 128 * 4), bb.DeviceBuffer(n * 8)
     try:
-        pages = bb.Pages([kv.ptr] * 193, [kv.ptr] * 193, [32] * 193, [])
+        pages = bb.Pages([kv.ptr] * 385, [kv.ptr] * 385, [32] * 385, [])
         with pytest.raises(bb.PaHipError, match="more slots than the scratch holds"):
             bb.attn_noalloc(bb.make_shape(nkv, rows, 128, bb.FMT_Q8_0), pages, dq.ptr, do.ptr, dml.ptr, dml.ptr + n * 4)
     finally:
